@@ -1,0 +1,208 @@
+"""Benchmark of the VCSR SpMM hot path on one MI355X.
+
+Workload (the headline): banded FEM-like A, 62,451^2,
+~3.94M nnz (synthetic, seed 0), dense B 62,451 x 128 FP32 U[-1,1), VCSR
+layout S with segw=4, bundle=64, tileK=64, built and uploaded before timing.
+
+A step is one complete SpMM C = A*B on device-resident inputs: reset C (the
+VCSR kernel accumulates into C, as the reference's does) and run the
+segmented-streaming kernel.  K steps are timed between HIP events after W
+warm-up steps; `value` is 2*nnz*O*K / that time.  The kernel alone is then
+timed per launch with events on its stream (the reference's convention,
+src/kernels.cu:153-162) for `kernel_ms` and the roofline.
+
+Prints ONE JSON line.  Multi-GPU runs are not part of this build.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    # name: (cfg, O, segw, bundle, tileK, layout, B distribution)
+    "cfg2": (2, 128, 4, 64, 64, 1, 0),
+    "cfg2_o8": (2, 8, 4, 64, 64, 1, 0),
+    "cfg2_o32": (2, 32, 4, 64, 64, 1, 0),
+    "cfg2_o512": (2, 512, 4, 64, 64, 1, 0),
+    "cfg3": (3, 128, 4, 64, 128, 1, 0),
+    "cfg3_o8": (3, 8, 4, 64, 128, 1, 0),
+    "cfg4": (4, 256, 4, 64, 128, 1, 0),
+    "cfg4_segw8": (4, 256, 8, 64, 128, 1, 0),
+    "cfg5": (5, 512, 16, 16, 64, 2, 1),
+}
+
+
+def _load_product():
+    import importlib.util
+    name = "vcsr_spmm_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(
+        name, os.path.join(ROOT, "vcsr-spmm_amd", "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(orc, csr, B, seconds):
+    """The oracle's single-thread FP32 CSR SpMM (reference loop order) on the
+    same matrix and B, repeated until `seconds` of CPU work."""
+    flop = 2.0 * csr.nnz * B.shape[1]
+    reps, t_total = 0, 0.0
+    while t_total < seconds and reps < 1000:
+        t0 = time.perf_counter()
+        orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    return flop * reps / t_total / 1e9, reps, t_total
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--algo", default="vcsr", choices=["vcsr", "mfma", "csr"])
+    ap.add_argument("--tileK", type=int, default=None)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); multi-GPU sharding is design-only", file=sys.stderr)
+        sys.exit(2)
+
+    vs = _load_product()
+    vs.load_library()
+    if vs.device_count() <= 0:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(2)
+    from oracle import oracle as orc
+
+    cfg, O, segw, bundle, tileK, layout, dist = CONFIGS[args.config]
+    if args.tileK:
+        tileK = args.tileK
+    log(f"bench: {args.config} algo={args.algo} O={O} segw={segw} bundle={bundle} "
+        f"tileK={tileK} device={vs.device_name()}")
+    t0 = time.perf_counter()
+    csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
+    B = vs.gen_dense(cfg, dist, csr.N, O)
+    log(f"bench: matrix {csr.M}x{csr.N} nnz={csr.nnz} generated in {time.perf_counter()-t0:.2f}s")
+    st = vs.Stream()
+    dB = vs.DeviceArray.from_numpy(B, st)
+    dC = vs.DeviceArray((csr.M, O), np.float32)
+    fmt = None
+    if args.algo == "csr":
+        d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
+        d_col = vs.DeviceArray.from_numpy(csr.col, st)
+        d_val = vs.DeviceArray.from_numpy(csr.val, st)
+
+        def kernel(timed=False):
+            return vs.run_csr_spmm_gpu(csr.M, d_rp, d_col, d_val, dB, O, dC, st, timed=timed)
+    else:
+        t0 = time.perf_counter()
+        fmt = vs.build_vcsr(csr, segw, bundle, layout)
+        tb = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        fmt.upload(st)
+        log(f"bench: VCSR layout={layout} groups={fmt.num_groups} slots={fmt.num_slots} "
+            f"build {tb*1e3:.1f} ms upload {(time.perf_counter()-t0)*1e3:.1f} ms")
+        if args.algo == "vcsr":
+            def kernel(timed=False):
+                return vs.run_vcsr_spmm_gpu(fmt, dB, O, tileK, dC, st, timed=timed)
+        else:
+            def kernel(timed=False):
+                return vs.run_vcsr_tc_spmm_gpu(fmt, dB, O, dC, st, timed=timed)
+
+    def step():
+        dC.zero(st)
+        kernel()
+
+    for _ in range(args.warmup):
+        step()
+    st.sync()
+    ev0, ev1 = vs.Event(), vs.Event()
+    lib = vs.load_library()
+    lib.vcsr_device_sync()
+    ev0.record(st)
+    for _ in range(args.steps):
+        step()
+    ev1.record(st)
+    total_ms = ev0.elapsed_ms(ev1)
+    lib.vcsr_device_sync()
+    C = dC.numpy(st)
+
+    # Correctness of the last step: sampled rows against the oracle (double).
+    rng = np.random.default_rng(0)
+    rows = np.unique(rng.choice(csr.M, size=min(512, csr.M), replace=False))
+    rp = np.concatenate([[0], np.cumsum(np.diff(csr.row_ptr)[rows])]).astype(np.int32)
+    cols = np.concatenate([csr.col[csr.row_ptr[r]:csr.row_ptr[r + 1]] for r in rows])
+    vals = np.concatenate([csr.val[csr.row_ptr[r]:csr.row_ptr[r + 1]] for r in rows])
+    ref = orc.spmm_f64(len(rows), rp, cols.astype(np.int32), vals.astype(np.float32), B)
+    rel = float(np.linalg.norm(C[rows] - ref) / max(np.linalg.norm(ref), 1e-300))
+    check = "pass" if rel <= 1e-5 else "FAIL"
+    log(f"bench: sampled-row rel L2 vs oracle {rel:.2e} ({check})")
+
+    # Kernel-only duration: events around each launch on the kernel's stream.
+    kms = []
+    for _ in range(max(10, min(args.steps, 100))):
+        kms.append(kernel(timed=True))
+    kernel_ms = float(np.mean(kms))
+
+    flop = 2.0 * csr.nnz * O
+    ms_per_step = total_ms / args.steps
+    value = flop / (ms_per_step * 1e-3) / 1e9
+    bytes_alg = 4.0 * (csr.M + 1) + 8.0 * csr.nnz + 4.0 * csr.N * O + 4.0 * csr.M * O
+    achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
+    out = {
+        "metric": "SpMM GFLOP/s (2*nnz*O/t) + % of HBM roofline, FP32, O=128, 1xMI355X",
+        "value": round(value, 2),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: {csr.M}x{csr.N} nnz={csr.nnz} O={O}",
+                   "algo": args.algo, "segw": segw, "bundle": bundle, "tileK": tileK,
+                   "layout": ["H", "S", "TC"][layout] if args.algo != "csr" else "csr",
+                   "step": "C reset + SpMM kernel"},
+        "kernel_ms": round(kernel_ms, 5),
+        "kernel_gflops": round(flop / (kernel_ms * 1e-3) / 1e9, 2),
+        "check": {"rel_l2_sampled_rows": rel, "result": check},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_alg": bytes_alg},
+    }
+    if not args.no_cpu_baseline:
+        gf, reps, secs = cpu_baseline(orc, csr, B, args.cpu_seconds)
+        out["cpu_baseline"] = {"value": round(gf, 3), "unit": "GFLOP/s", "cores": 1,
+                               "kind": "port",
+                               "sample": f"full {args.config} matrix x B (O={O}), {reps} reps, "
+                                         f"{secs:.1f}s, oracle FP32 CSR SpMM single thread"}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

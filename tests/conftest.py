@@ -1,0 +1,104 @@
+"""Shared fixtures: the product binding (vcsr-spmm_amd, via ctypes), the CPU
+oracle (test infrastructure), and the tolerance check of the north star."""
+from __future__ import annotations
+
+import importlib.util
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box only)")
+
+
+def load_product():
+    """Imports vcsr-spmm_amd/ (a directory name with a hyphen) as vcsr_spmm_amd."""
+    name = "vcsr_spmm_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    path = os.path.join(ROOT, "vcsr-spmm_amd", "__init__.py")
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@pytest.fixture(scope="session")
+def vs():
+    mod = load_product()
+    mod.load_library()
+    return mod
+
+
+@pytest.fixture(scope="session")
+def orc():
+    from oracle import oracle
+    oracle.oracle_lib()
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def gpu(vs):
+    if vs.device_count() <= 0:
+        pytest.fail("no GPU visible to the library (gpu tests run on the GPU box)")
+    return vs
+
+
+def tolerance_report(C, ref64, row_l1, bmax):
+    """rel L2 <= 1e-5 and, per row r, max-abs error
+    <= 1e-4 * ||A_r||_1 * max|B|.  Returns (rel_l2, worst max-abs/tol)."""
+    C = np.asarray(C, dtype=np.float64)
+    diff = C - ref64
+    den = np.linalg.norm(ref64)
+    rel = np.linalg.norm(diff) / den if den > 0 else np.linalg.norm(diff)
+    tol = 1e-4 * np.asarray(row_l1, dtype=np.float64)[:, None] * bmax
+    err = np.abs(diff)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ratio = np.where(tol > 0, err / tol, np.where(err > 0, np.inf, 0.0))
+    return float(rel), float(ratio.max()) if ratio.size else 0.0
+
+
+def row_abs_sums(row_ptr, val):
+    """||A_r||_1 for every row (empty rows give 0)."""
+    M = len(row_ptr) - 1
+    rows = np.repeat(np.arange(M), np.diff(row_ptr))
+    return np.bincount(rows, weights=np.abs(np.asarray(val, dtype=np.float64)), minlength=M)
+
+
+def assert_within_tolerance(C, ref64, row_ptr, val, B, what=""):
+    row_l1 = row_abs_sums(row_ptr, val)
+    bmax = float(np.abs(B).max()) if B.size else 0.0
+    rel, worst = tolerance_report(C, ref64, row_l1, bmax)
+    assert rel <= 1e-5, f"{what}: rel L2 {rel:.3e} > 1e-5"
+    assert worst <= 1.0, f"{what}: max-abs error {worst:.3f} x tolerance"
+    return rel, worst
+
+
+def random_csr(rng, M, N, density=0.05, dup_rate=0.0, empty_rows=0.0, max_row=None):
+    """Random CSR arrays (row_ptr, col, val) as the reference would build
+    them from an unsorted COO: columns sorted per row, duplicates allowed."""
+    rows, cols = [], []
+    for r in range(M):
+        if rng.random() < empty_rows:
+            continue
+        k = rng.binomial(N, density) if max_row is None else rng.integers(0, max_row + 1)
+        k = min(k, N)
+        c = rng.choice(N, size=k, replace=False) if k else np.zeros(0, np.int64)
+        if dup_rate and k:
+            extra = c[rng.random(k) < dup_rate]
+            c = np.concatenate([c, extra])
+        rng.shuffle(c)
+        rows.extend([r] * len(c))
+        cols.extend(c.tolist())
+    rows = np.array(rows, dtype=np.int32)
+    cols = np.array(cols, dtype=np.int32)
+    vals = rng.uniform(-1, 1, size=len(rows)).astype(np.float32)
+    return rows, cols, vals

@@ -1,0 +1,200 @@
+"""GPU parity: every HIP kernel, called through the C ABI, against the CPU
+oracle (oracle/vcsr_oracle.cpp) on the same seeded inputs.
+
+  * naive CSR: same loop order and FMA as the oracle's FP32 SpMM -> bit-exact;
+  * VCSR streaming and FP32-MFMA kernels: different summation order and FP32
+    atomics -> north-star tolerance (rel L2 <= 1e-5, per-row max-abs <=
+    1e-4 * ||A_r||_1 * max|B|) against the oracle's double-accumulated sum,
+    and the same against its FP32 sum;
+  * full-size configs: per-row oracle check on sampled rows plus the
+    size-independent column-sum identity sum_r C[r,:] = (1^T A) B.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_within_tolerance, random_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(vs, orc, rng, M, N, density=0.05, dup_rate=0.0, empty_rows=0.0):
+    rows, cols, vals = random_csr(rng, M, N, density, dup_rate, empty_rows)
+    coo = vs.Coo.from_arrays(M, N, rows, cols, vals)
+    return vs.coo_to_csr(coo)
+
+
+def _device_csr(vs, csr, st):
+    return (vs.DeviceArray.from_numpy(csr.row_ptr, st), vs.DeviceArray.from_numpy(csr.col, st),
+            vs.DeviceArray.from_numpy(csr.val, st))
+
+
+def _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=64):
+    """Runs one kernel through the C ABI and returns C as numpy."""
+    M, O = csr.M, B.shape[1]
+    dB = vs.DeviceArray.from_numpy(B, st)
+    dC = vs.DeviceArray((M, O), np.float32)
+    dC.zero(st)
+    if kind == "csr":
+        rp, col, val = _device_csr(vs, csr, st)
+        ms = vs.run_csr_spmm_gpu(M, rp, col, val, dB, O, dC, st, timed=True)
+    else:
+        fmt = vs.build_vcsr(csr, segw, bundle, layout)
+        fmt.upload(st)
+        if kind == "vcsr":
+            ms = vs.run_vcsr_spmm_gpu(fmt, dB, O, tileK, dC, st, timed=True)
+        else:
+            ms = vs.run_vcsr_tc_spmm_gpu(fmt, dB, O, dC, st, timed=True)
+    assert ms is not None and ms >= 0.0
+    st.sync()
+    return dC.numpy(st)
+
+
+@pytest.fixture(scope="module")
+def st(gpu):
+    return gpu.Stream()
+
+
+# ----------------------------------------------------------- naive CSR
+@pytest.mark.parametrize("O", [1, 7, 32, 128])
+def test_csr_naive_bit_exact_random(gpu, orc, st, O):
+    vs = gpu
+    rng = np.random.default_rng(100 + O)
+    csr = _case(vs, orc, rng, 300, 257, density=0.04, dup_rate=0.1, empty_rows=0.1)
+    B = vs.gen_dense(7, 0, csr.N, O)
+    C = _run(vs, "csr", csr, B, st)
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))
+
+
+def test_csr_naive_bit_exact_cfg1(gpu, orc, st):
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(1, 0))
+    B = vs.gen_dense(1, 0, csr.N, 32)
+    C = _run(vs, "csr", csr, B, st)
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))
+
+
+# ---------------------------------------------------- VCSR kernels, small
+KERNELS = [("vcsr", 1), ("vcsr", 0), ("mfma", 1), ("mfma", 0), ("mfma", 2), ("vcsr", 2)]
+
+
+@pytest.mark.parametrize("kind,layout", KERNELS)
+@pytest.mark.parametrize("O", [1, 8, 33, 128, 200])
+def test_vcsr_kernels_random(gpu, orc, st, kind, layout, O):
+    vs = gpu
+    rng = np.random.default_rng(1000 + 10 * O + layout)
+    csr = _case(vs, orc, rng, 257, 203, density=0.05, dup_rate=0.05, empty_rows=0.1)
+    B = vs.gen_dense(3, 0, csr.N, O)
+    C = _run(vs, kind, csr, B, st, layout=layout, segw=4, bundle=64, tileK=64)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert_within_tolerance(C, ref64, csr.row_ptr, csr.val, B, f"{kind}/L{layout}/O{O}")
+    ref32 = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert_within_tolerance(C, ref32.astype(np.float64), csr.row_ptr, csr.val, B, "vs f32")
+
+
+@pytest.mark.parametrize("kind", ["vcsr", "mfma"])
+@pytest.mark.parametrize("segw,bundle,tileK", [(1, 64, 32), (3, 64, 100), (8, 64, 128),
+                                               (16, 32, 64), (5, 20, 32), (20, 64, 256),
+                                               (4, 128, 64), (4, 1, 32), (33, 16, 64)])
+def test_vcsr_kernels_shapes(gpu, orc, st, kind, segw, bundle, tileK):
+    vs = gpu
+    rng = np.random.default_rng(segw * 1000 + bundle * 10 + tileK)
+    csr = _case(vs, orc, rng, 190, 150, density=0.08, dup_rate=0.1, empty_rows=0.05)
+    O = 70
+    B = vs.gen_dense(5, 1, csr.N, O)
+    C = _run(vs, kind, csr, B, st, layout=1, segw=segw, bundle=bundle, tileK=tileK)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert_within_tolerance(C, ref64, csr.row_ptr, csr.val, B, f"{kind} segw{segw} b{bundle}")
+
+
+@pytest.mark.parametrize("kind,layout", KERNELS)
+def test_vcsr_kernels_cfg1(gpu, orc, st, kind, layout):
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(1, 0))
+    B = vs.gen_dense(1, 0, csr.N, 32)
+    C = _run(vs, kind, csr, B, st, layout=layout, segw=4, bundle=64, tileK=64)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert_within_tolerance(C, ref64, csr.row_ptr, csr.val, B, f"cfg1 {kind}/L{layout}")
+
+
+def test_vcsr_empty_and_degenerate(gpu, orc, st):
+    vs = gpu
+    # no nonzeros at all, and a matrix whose N is not a multiple of segw
+    for M, N in [(5, 3), (64, 1), (1, 17)]:
+        csr = vs.Csr.from_arrays(M, N, np.zeros(M + 1, np.int32), np.zeros(0, np.int32),
+                                 np.zeros(0, np.float32))
+        B = vs.gen_dense(2, 0, N, 9)
+        for kind in ("csr", "vcsr", "mfma"):
+            C = _run(vs, kind, csr, B, st)
+            assert not C.any()
+    rng = np.random.default_rng(5)
+    csr = _case(vs, orc, rng, 40, 13, density=0.3)
+    B = vs.gen_dense(2, 0, csr.N, 9)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    for kind in ("vcsr", "mfma"):
+        C = _run(vs, kind, csr, B, st, segw=4)
+        assert_within_tolerance(C, ref64, csr.row_ptr, csr.val, B, kind)
+
+
+def test_vcsr_repeat_runs_agree(gpu, orc, st):
+    """Atomic flush order varies between runs; results stay within tolerance."""
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(1, 0))
+    B = vs.gen_dense(1, 0, csr.N, 128)
+    runs = [_run(vs, "vcsr", csr, B, st) for _ in range(3)]
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    for C in runs:
+        assert_within_tolerance(C, ref64, csr.row_ptr, csr.val, B, "repeat")
+
+
+# ------------------------------------------------- full-size configurations
+def _rowsample_check(vs, orc, csr, B, C, nrows, seed):
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([rng.choice(csr.M, size=min(nrows, csr.M), replace=False),
+                                     [0, csr.M - 1], [int(np.argmax(np.diff(csr.row_ptr)))]]))
+    rp = np.zeros(len(rows) + 1, np.int64)
+    cols, vals = [], []
+    for i, r in enumerate(rows):
+        s, e = csr.row_ptr[r], csr.row_ptr[r + 1]
+        cols.append(csr.col[s:e])
+        vals.append(csr.val[s:e])
+        rp[i + 1] = rp[i] + (e - s)
+    cols = np.concatenate(cols).astype(np.int32)
+    vals = np.concatenate(vals).astype(np.float32)
+    rp = rp.astype(np.int32)
+    ref64 = orc.spmm_f64(len(rows), rp, cols, vals, B)
+    assert_within_tolerance(C[rows], ref64, rp, vals, B, "sampled rows")
+
+
+def _colsum_check(csr, B, C):
+    """sum_r C[r,:] == (1^T A) B, in double: pins all of C in aggregate."""
+    s = np.bincount(csr.col, weights=csr.val.astype(np.float64), minlength=csr.N)
+    want = s @ B.astype(np.float64)
+    got = C.astype(np.float64).sum(axis=0)
+    scale = np.abs(csr.val).astype(np.float64).sum() * float(np.abs(B).max())
+    assert np.max(np.abs(got - want)) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("cfg,O,segw,tileK,layout", [(2, 128, 4, 64, 1), (3, 128, 4, 128, 1),
+                                                     (2, 8, 4, 64, 1), (5, 64, 16, 64, 2)])
+@pytest.mark.parametrize("kind", ["vcsr", "mfma"])
+def test_full_size_configs(gpu, orc, st, cfg, O, segw, tileK, layout, kind):
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
+    B = vs.gen_dense(cfg, 1 if cfg == 5 else 0, csr.N, O)
+    bundle = 16 if layout == 2 else 64
+    C = _run(vs, kind, csr, B, st, layout=layout, segw=segw, bundle=bundle, tileK=tileK)
+    _rowsample_check(vs, orc, csr, B, C, 2000, cfg)
+    _colsum_check(csr, B, C)
+
+
+def test_full_size_csr_naive_cfg2(gpu, orc, st):
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(2, 0))
+    B = vs.gen_dense(2, 0, csr.N, 128)
+    C = _run(vs, "csr", csr, B, st)
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))

@@ -1,0 +1,45 @@
+// fmt_internal.hpp - definition of the opaque handles of include/vcsr_spmm.h,
+// shared by the host entry points (capi_host.cpp, g++) and the device entry
+// points (device/runtime.hip, hipcc).  Device memory is held as plain
+// pointers so this header needs no HIP include.
+#pragma once
+
+#include <cstdint>
+#include <string>
+
+#include "host/core.hpp"
+
+// Device copy of a VCSR format plus the derived work list the kernels use.
+struct DeviceFmt {
+    bool uploaded = false;
+    int device = -1;
+    int32_t* group_ptr = nullptr;       // G+1
+    int32_t* group_depth = nullptr;     // G
+    int32_t* group_seg_base = nullptr;  // G
+    int32_t* group_rows = nullptr;      // G*bundle
+    int32_t* group_nact = nullptr;      // G: lanes with >= 1 entry (a prefix of the lanes)
+    int32_t* lcol = nullptr;            // P
+    float* val = nullptr;               // P
+    int32_t* items = nullptr;           // 2*n_items: [first group, end group) per work item
+    int32_t n_items = 0;
+    int32_t max_depth = 0;
+};
+
+struct vcsr_coo {
+    vcsr::Coo coo;
+};
+struct vcsr_csr {
+    vcsr::Csr csr;
+};
+struct vcsr_fmt {
+    vcsr::Vcsr v;
+    DeviceFmt dev;
+};
+
+namespace vcsr {
+// Records the message of a failing call for vcsr_last_error() and returns code.
+int set_error(int code, const std::string& msg);
+void clear_error();
+// Releases the device part of a format (device/runtime.hip).
+void free_device_fmt(DeviceFmt& d);
+}  // namespace vcsr
