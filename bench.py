@@ -78,7 +78,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
-    ap.add_argument("--algo", default="vcsr", choices=["vcsr", "mfma", "csr"])
+    ap.add_argument("--algo", default="vcsr", choices=["vcsr", "row", "segment", "mfma", "csr"])
     ap.add_argument("--tileK", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -109,10 +109,14 @@ def main():
     dB = vs.DeviceArray.from_numpy(B, st)
     dC = vs.DeviceArray((csr.M, O), np.float32)
     fmt = None
+    # Kernels that write every C element themselves need no reset per step;
+    # the accumulate-into-C kernels get a C reset inside the timed step.
+    needs_reset = True
     if args.algo == "csr":
         d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
         d_col = vs.DeviceArray.from_numpy(csr.col, st)
         d_val = vs.DeviceArray.from_numpy(csr.val, st)
+        needs_reset = False  # zeroes its own rows (src/kernels.cu:25)
 
         def kernel(timed=False):
             return vs.run_csr_spmm_gpu(csr.M, d_rp, d_col, d_val, dB, O, dC, st, timed=timed)
@@ -124,15 +128,18 @@ def main():
         fmt.upload(st)
         log(f"bench: VCSR layout={layout} groups={fmt.num_groups} slots={fmt.num_slots} "
             f"build {tb*1e3:.1f} ms upload {(time.perf_counter()-t0)*1e3:.1f} ms")
-        if args.algo == "vcsr":
-            def kernel(timed=False):
-                return vs.run_vcsr_spmm_gpu(fmt, dB, O, tileK, dC, st, timed=timed)
-        else:
-            def kernel(timed=False):
-                return vs.run_vcsr_tc_spmm_gpu(fmt, dB, O, dC, st, timed=timed)
+        kern = {"vcsr": vs.KERNEL_AUTO, "row": vs.KERNEL_ROW, "segment": vs.KERNEL_SEGMENT,
+                "mfma": vs.KERNEL_MFMA}[args.algo]
+        overwrite = kern in (vs.KERNEL_AUTO, vs.KERNEL_ROW)
+        needs_reset = not overwrite
+
+        def kernel(timed=False):
+            return vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, tileK, dC, st, timed=timed, kernel=kern,
+                                           accumulate=not overwrite)
 
     def step():
-        dC.zero(st)
+        if needs_reset:
+            dC.zero(st)
         kernel()
 
     for _ in range(args.warmup):
@@ -187,7 +194,8 @@ def main():
         "config": {"workload": f"{args.config}: {csr.M}x{csr.N} nnz={csr.nnz} O={O}",
                    "algo": args.algo, "segw": segw, "bundle": bundle, "tileK": tileK,
                    "layout": ["H", "S", "TC"][layout] if args.algo != "csr" else "csr",
-                   "step": "C reset + SpMM kernel"},
+                   "step": "C reset + SpMM kernel (C += A*B)" if needs_reset
+                   else "SpMM kernel writing C = A*B"},
         "kernel_ms": round(kernel_ms, 5),
         "kernel_gflops": round(flop / (kernel_ms * 1e-3) / 1e9, 2),
         "check": {"rel_l2_sampled_rows": rel, "result": check},

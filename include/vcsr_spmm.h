@@ -163,6 +163,30 @@ int spmm_csr_naive(int32_t M, const int32_t* d_rowptr, const int32_t* d_col,
 int spmm_vcsr(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
               float* dC, void* stream, float* ms);
 
+/* Kernel selection of spmm_vcsr_ex (all consume the same uploaded format). */
+enum {
+    VCSR_KERNEL_AUTO = 0,    /* the fastest kernel for the format (currently ROW) */
+    VCSR_KERNEL_SEGMENT = 1, /* segment-major streaming on the vector ALUs, B tile
+                                in LDS, C flushed with FP32 atomics per group   */
+    VCSR_KERNEL_MFMA = 2,    /* segment-major, group collapsed to a dense tile on
+                                FP32 MFMA, C flushed with FP32 atomics          */
+    VCSR_KERNEL_ROW = 3      /* row-stationary: one wavefront per C row walks the
+                                row's (group, lane) slots; C written once, no
+                                atomics                                         */
+};
+
+/* spmm_vcsr with an explicit kernel and C semantics: accumulate = 1 gives
+ * C += A*B (the reference's semantics), accumulate = 0 gives C = A*B without
+ * a separate reset (the ROW kernel writes every row once; the segment-major
+ * kernels clear C on the stream first).  tileK applies to the segment-major
+ * kernels.  Calls on one format must not overlap in time: the ROW kernel keeps
+ * a scratch buffer for the partial sums of very long rows in the format.
+ * No reference counterpart (the reference selects kernels by --algo in
+ * src/main.cpp:119-163 and always accumulates). */
+int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
+                 float* dC, void* stream, float* ms, int32_t kernel,
+                 int32_t accumulate);
+
 /* C += A*B on FP32 MFMA: every group is collapsed to a dense bundle x segw
  * tile and multiplied by the segment's B tile on the matrix cores (FP32 in,
  * FP32 accumulate).  Meant for dense sub-blocks (layout TC); valid for any

@@ -44,6 +44,12 @@ def _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=64):
         fmt.upload(st)
         if kind == "vcsr":
             ms = vs.run_vcsr_spmm_gpu(fmt, dB, O, tileK, dC, st, timed=True)
+        elif kind == "segment":
+            ms = vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, tileK, dC, st, timed=True,
+                                         kernel=vs.KERNEL_SEGMENT)
+        elif kind == "row":
+            ms = vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, tileK, dC, st, timed=True,
+                                         kernel=vs.KERNEL_ROW)
         else:
             ms = vs.run_vcsr_tc_spmm_gpu(fmt, dB, O, dC, st, timed=True)
     assert ms is not None and ms >= 0.0
@@ -78,7 +84,8 @@ def test_csr_naive_bit_exact_cfg1(gpu, orc, st):
 
 
 # ---------------------------------------------------- VCSR kernels, small
-KERNELS = [("vcsr", 1), ("vcsr", 0), ("mfma", 1), ("mfma", 0), ("mfma", 2), ("vcsr", 2)]
+KERNELS = [("vcsr", 1), ("vcsr", 0), ("mfma", 1), ("mfma", 0), ("mfma", 2), ("vcsr", 2),
+           ("segment", 1), ("segment", 0), ("segment", 2), ("row", 1), ("row", 0), ("row", 2)]
 
 
 @pytest.mark.parametrize("kind,layout", KERNELS)
@@ -95,7 +102,7 @@ def test_vcsr_kernels_random(gpu, orc, st, kind, layout, O):
     assert_within_tolerance(C, ref32.astype(np.float64), csr.row_ptr, csr.val, B, "vs f32")
 
 
-@pytest.mark.parametrize("kind", ["vcsr", "mfma"])
+@pytest.mark.parametrize("kind", ["segment", "mfma", "row"])
 @pytest.mark.parametrize("segw,bundle,tileK", [(1, 64, 32), (3, 64, 100), (8, 64, 128),
                                                (16, 32, 64), (5, 20, 32), (20, 64, 256),
                                                (4, 128, 64), (4, 1, 32), (33, 16, 64)])
@@ -180,7 +187,7 @@ def _colsum_check(csr, B, C):
 
 @pytest.mark.parametrize("cfg,O,segw,tileK,layout", [(2, 128, 4, 64, 1), (3, 128, 4, 128, 1),
                                                      (2, 8, 4, 64, 1), (5, 64, 16, 64, 2)])
-@pytest.mark.parametrize("kind", ["vcsr", "mfma"])
+@pytest.mark.parametrize("kind", ["segment", "mfma", "row"])
 def test_full_size_configs(gpu, orc, st, cfg, O, segw, tileK, layout, kind):
     vs = gpu
     csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
@@ -198,3 +205,69 @@ def test_full_size_csr_naive_cfg2(gpu, orc, st):
     C = _run(vs, "csr", csr, B, st)
     ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
     assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------ row-stationary kernel modes
+def _ex(vs, fmt, B, C0, st, kernel, accumulate, tileK=64):
+    dB = vs.DeviceArray.from_numpy(B, st)
+    dC = vs.DeviceArray.from_numpy(C0, st)
+    vs.run_vcsr_spmm_gpu_ex(fmt, dB, B.shape[1], tileK, dC, st, timed=True, kernel=kernel,
+                            accumulate=accumulate)
+    st.sync()
+    return dC.numpy(st)
+
+
+@pytest.mark.parametrize("kernel", [1, 2, 3])
+@pytest.mark.parametrize("O", [5, 64, 130, 256, 300])
+def test_accumulate_and_overwrite(gpu, orc, st, kernel, O):
+    """accumulate=1 adds A*B to the C it is given; accumulate=0 replaces it."""
+    vs = gpu
+    rng = np.random.default_rng(77 + O)
+    csr = _case(vs, orc, rng, 150, 120, density=0.06, dup_rate=0.05, empty_rows=0.2)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.upload(st)
+    B = vs.gen_dense(9, 0, csr.N, O)
+    C0 = rng.uniform(-2, 2, size=(csr.M, O)).astype(np.float32)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    got = _ex(vs, fmt, B, C0, st, kernel, True)
+    assert_within_tolerance(got - C0, ref64, csr.row_ptr, csr.val, B, "accumulate")
+    got = _ex(vs, fmt, B, C0, st, kernel, False)
+    assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, "overwrite")
+
+
+@pytest.mark.parametrize("accumulate", [True, False])
+def test_row_kernel_split_rows(gpu, orc, st, accumulate):
+    """Rows with more (row, segment) pairs than one wave takes are split into
+    chunks and reduced by a second kernel; run it twice (scratch reuse) and
+    with a wider O (scratch growth)."""
+    vs = gpu
+    rng = np.random.default_rng(3)
+    M, N = 40, 3000
+    rows, cols, vals = random_csr(rng, M, N, density=0.01)
+    dense_rows = [0, 7, 39]
+    for r in dense_rows:  # every column: N/segw = 750 pairs > one chunk
+        rows = np.concatenate([rows, np.full(N, r, np.int32)])
+        cols = np.concatenate([cols, np.arange(N, dtype=np.int32)])
+        vals = np.concatenate([vals, rng.uniform(-1, 1, N).astype(np.float32)])
+    csr = vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.upload(st)
+    for O in (64, 64, 200):
+        B = vs.gen_dense(O, 0, N, O)
+        C0 = np.ones((M, O), np.float32)
+        ref64 = orc.spmm_f64(M, csr.row_ptr, csr.col, csr.val, B)
+        got = _ex(vs, fmt, B, C0, st, vs.KERNEL_ROW, accumulate)
+        if accumulate:
+            got = got - C0
+        assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"split O={O}")
+
+
+@pytest.mark.parametrize("cfg,O,layout", [(3, 128, 1), (4, 256, 1), (5, 512, 2)])
+def test_full_size_row_kernel(gpu, orc, st, cfg, O, layout):
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
+    B = vs.gen_dense(cfg, 1 if cfg == 5 else 0, csr.N, O)
+    segw, bundle = (16, 16) if layout == 2 else (4, 64)
+    C = _run(vs, "row", csr, B, st, layout=layout, segw=segw, bundle=bundle, tileK=128)
+    _rowsample_check(vs, orc, csr, B, C, 1500, cfg)
+    _colsum_check(csr, B, C)

@@ -34,13 +34,14 @@ CLI_PATH = os.path.join(_HERE, "bin", "spmm_vcsr")
 
 VCSR_OK, VCSR_EINVAL, VCSR_EIO, VCSR_ENOMEM, VCSR_EDEVICE, VCSR_ERANGE, VCSR_ESTATE = range(7)
 LAYOUT_H, LAYOUT_S, LAYOUT_TC = 0, 1, 2
+KERNEL_AUTO, KERNEL_SEGMENT, KERNEL_MFMA, KERNEL_ROW = 0, 1, 2, 3
 
 # Every symbol include/vcsr_spmm.h declares (checked by the CPU test suite).
 EXPORTS = (
     "vcsr_last_error vcsr_version vcsr_mtx_read vcsr_coo_create vcsr_coo_view_get "
     "vcsr_coo_free vcsr_gen_coo vcsr_gen_dense vcsr_coo_to_csr vcsr_csr_create "
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
-    "vcsr_fmt_free spmm_csr_naive spmm_vcsr spmm_vcsr_mfma spmm_csr_cpu "
+    "vcsr_fmt_free spmm_csr_naive spmm_vcsr spmm_vcsr_ex spmm_vcsr_mfma spmm_csr_cpu "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
     "vcsr_memcpy_d2h vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
     "vcsr_stream_sync vcsr_device_sync vcsr_event_create vcsr_event_destroy "
@@ -108,6 +109,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "vcsr_fmt_free": (None, [P]),
         "spmm_csr_naive": (C.c_int, [I32, P, P, P, P, I32, P, P, pF]),
         "spmm_vcsr": (C.c_int, [P, P, I32, I32, P, P, pF]),
+        "spmm_vcsr_ex": (C.c_int, [P, P, I32, I32, P, P, pF, I32, I32]),
         "spmm_vcsr_mfma": (C.c_int, [P, P, I32, P, P, pF]),
         "spmm_csr_cpu": (C.c_int, [I32, P, P, P, P, I32, P, I32]),
         "vcsr_device_count": (C.c_int, [pI]),
@@ -382,10 +384,6 @@ class DeviceArray:
             self.ptr = C.c_void_p()
 
 
-def _ms_arg(timed: bool):
-    return C.byref(C.c_float(0)) if timed else None
-
-
 def run_csr_spmm_gpu(M, d_rowptr, d_col, d_val, dB, O, dC, stream=None, timed=False):
     """C = A*B (overwrites C).  Returns kernel ms when timed (synchronous)."""
     ms = C.c_float(0)
@@ -411,3 +409,13 @@ def run_vcsr_tc_spmm_gpu(fmt: Vcsr, dB, O, dC, stream=None, timed=False):
 
 
 run_vcsr_mfma_spmm_gpu = run_vcsr_tc_spmm_gpu
+
+
+def run_vcsr_spmm_gpu_ex(fmt: Vcsr, dB, O, tileK, dC, stream=None, timed=False,
+                         kernel=KERNEL_AUTO, accumulate=True):
+    """SpMM with an explicit kernel; accumulate=False computes C = A*B."""
+    ms = C.c_float(0)
+    _check(load_library().spmm_vcsr_ex(fmt._h, dB.ptr, O, tileK, dC.ptr, _sp(stream),
+                                       C.byref(ms) if timed else None, kernel,
+                                       1 if accumulate else 0))
+    return ms.value if timed else None

@@ -27,4 +27,16 @@ hipError_t launch_vcsr_mfma(const Vcsr& v, const DeviceFmt& d, const float* B, i
 // Column-block width (in 32-column MFMA blocks) used for a tileK request.
 int mfma_col_blocks(int32_t tileK, int32_t O);
 
+// vcsr_rowmajor.hip: row-stationary traversal of the VCSR slots; C = A*B
+// (accumulate = 0) or C += A*B (accumulate = 1).  Needs d.partials sized for
+// O when the format has split rows.
+hipError_t launch_vcsr_rowmajor(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                                float* C, int32_t accumulate, hipStream_t st);
+
+// A row-stationary work item covers at most this many (group, lane) pair
+// records (one per lane) and entries (the wave's LDS list); longer rows are
+// split into chunks whose partial sums a second kernel adds.
+constexpr int32_t kRowChunkPairs = 64;
+constexpr int32_t kRowChunkEntries = 512;
+
 }  // namespace vcsr

@@ -116,6 +116,86 @@ std::vector<int32_t> make_items(const vcsr::Vcsr& v, int max_lanes) {
     return items;
 }
 
+// Row-stationary view: the inverse of group_rows.  For every group g and
+// active lane l (row r = group_rows[g*bundle+l]) one record
+// {group_ptr[g]+l, group_seg_base[g], entries of the lane, r}, ordered by r
+// and, inside a row, by g (segment order).  A lane with more than
+// kRowChunkEntries entries (only possible with duplicate columns) becomes
+// several records over consecutive depth ranges.  Each row is cut greedily
+// into chunks of at most kRowChunkPairs records and kRowChunkEntries
+// entries; a row needing more than one chunk writes per-chunk partial sums
+// that a second kernel reduces.
+struct RowView {
+    std::vector<int32_t> pair_rec, row_items, split_rows;
+    int32_t n_partials = 0;
+};
+
+RowView make_row_view(const vcsr::Vcsr& v, const std::vector<int32_t>& nact) {
+    RowView rv;
+    const int32_t G = v.num_groups(), M = v.M, b = v.bundle;
+    const int32_t E = vcsr::kRowChunkEntries;
+    // Entry count of every active lane (entries are packed from depth 0).
+    std::vector<int64_t> lane_off((size_t)G + 1, 0);
+    for (int32_t g = 0; g < G; ++g) lane_off[(size_t)g + 1] = lane_off[(size_t)g] + nact[(size_t)g];
+    std::vector<int32_t> lane_cnt((size_t)lane_off[(size_t)G]);
+    std::vector<int64_t> ptr((size_t)M + 1, 0);
+    for (int32_t g = 0; g < G; ++g) {
+        const int32_t depth = v.group_depth[g];
+        for (int32_t l = 0; l < nact[(size_t)g]; ++l) {
+            const int32_t slot0 = v.group_ptr[g] + l;
+            int32_t cnt = 0;
+            while (cnt < depth && v.lcol[(size_t)slot0 + (size_t)cnt * b] >= 0) ++cnt;
+            lane_cnt[(size_t)(lane_off[(size_t)g] + l)] = cnt;
+            ptr[(size_t)v.group_rows[(size_t)g * b + l] + 1] += (cnt + E - 1) / E;
+        }
+    }
+    for (int32_t r = 0; r < M; ++r) ptr[(size_t)r + 1] += ptr[(size_t)r];
+    const int64_t nrec = ptr[(size_t)M];
+    if (nrec > INT32_MAX) throw vcsr::Error(VCSR_ERANGE, "too many (row, segment) pairs");
+    rv.pair_rec.resize((size_t)nrec * 4);
+    std::vector<int64_t> cur(ptr.begin(), ptr.end() - 1);
+    for (int32_t g = 0; g < G; ++g) {
+        for (int32_t l = 0; l < nact[(size_t)g]; ++l) {
+            const int32_t row = v.group_rows[(size_t)g * b + l];
+            const int32_t cnt = lane_cnt[(size_t)(lane_off[(size_t)g] + l)];
+            for (int32_t d0 = 0; d0 < cnt; d0 += E) {
+                int32_t* rec = rv.pair_rec.data() + 4 * cur[(size_t)row]++;
+                rec[0] = v.group_ptr[g] + l + d0 * b;
+                rec[1] = v.group_seg_base[g];
+                rec[2] = std::min(E, cnt - d0);
+                rec[3] = row;
+            }
+        }
+    }
+    rv.row_items.reserve((size_t)M * 4);
+    std::vector<int32_t> chunk_starts;
+    for (int32_t r = 0; r < M; ++r) {
+        const int32_t p0 = (int32_t)ptr[(size_t)r], p1 = (int32_t)ptr[(size_t)r + 1];
+        chunk_starts.clear();
+        chunk_starts.push_back(p0);
+        int32_t entries = 0;
+        for (int32_t p = p0; p < p1; ++p) {
+            const int32_t c = rv.pair_rec[(size_t)p * 4 + 2];
+            if (p - chunk_starts.back() == vcsr::kRowChunkPairs || entries + c > E) {
+                chunk_starts.push_back(p);
+                entries = 0;
+            }
+            entries += c;
+        }
+        if (chunk_starts.size() == 1) {
+            rv.row_items.insert(rv.row_items.end(), {r, p0, p1, -1});
+            continue;
+        }
+        const int32_t first = rv.n_partials;
+        for (size_t q = 0; q < chunk_starts.size(); ++q) {
+            const int32_t end = q + 1 < chunk_starts.size() ? chunk_starts[q + 1] : p1;
+            rv.row_items.insert(rv.row_items.end(), {r, chunk_starts[q], end, rv.n_partials++});
+        }
+        rv.split_rows.insert(rv.split_rows.end(), {r, first, rv.n_partials - first});
+    }
+    return rv;
+}
+
 }  // namespace
 
 namespace vcsr {
@@ -127,7 +207,8 @@ void free_device_fmt(DeviceFmt& d) {
     if (d.device >= 0 && d.device != cur) (void)hipSetDevice(d.device);
     for (void* p : {(void*)d.group_ptr, (void*)d.group_depth, (void*)d.group_seg_base,
                     (void*)d.group_rows, (void*)d.group_nact, (void*)d.lcol, (void*)d.val,
-                    (void*)d.items})
+                    (void*)d.items, (void*)d.pair_rec, (void*)d.row_items, (void*)d.split_rows,
+                    (void*)d.partials})
         if (p) (void)hipFree(p);
     if (d.device >= 0 && d.device != cur && cur >= 0) (void)hipSetDevice(cur);
     d = DeviceFmt();
@@ -157,6 +238,7 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             max_depth = std::max(max_depth, v.group_depth[g]);
         }
         std::vector<int32_t> items = make_items(v, 256);
+        RowView rv = make_row_view(v, nact);
         DeviceFmt d;
         hip_check(hipGetDevice(&d.device), "hipGetDevice");
         try {
@@ -171,6 +253,13 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.items = upload_array(items, st, "upload items");
             d.n_items = (int32_t)(items.size() / 2);
             d.max_depth = max_depth;
+            d.pair_rec = upload_array(rv.pair_rec, st, "upload pair records");
+            d.n_pairs = (int64_t)(rv.pair_rec.size() / 4);
+            d.row_items = upload_array(rv.row_items, st, "upload row items");
+            d.n_row_items = (int32_t)(rv.row_items.size() / 4);
+            d.split_rows = upload_array(rv.split_rows, st, "upload split rows");
+            d.n_split = (int32_t)(rv.split_rows.size() / 3);
+            d.n_partials = rv.n_partials;
             // The host vectors above must outlive the copies.
             hip_check(hipStreamSynchronize(st), "upload sync");
         } catch (...) {
@@ -195,35 +284,55 @@ int spmm_csr_naive(int32_t M, const int32_t* d_rowptr, const int32_t* d_col, con
     });
 }
 
-int spmm_vcsr(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK, float* dC,
-              void* stream, float* ms) {
+int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK, float* dC,
+                 void* stream, float* ms, int32_t kernel, int32_t accumulate) {
     return guarded([&] {
         need(fmt != nullptr, "null format");
         need(O >= 0, "negative O");
+        need(kernel >= VCSR_KERNEL_AUTO && kernel <= VCSR_KERNEL_ROW, "unknown kernel");
+        need(accumulate == 0 || accumulate == 1, "accumulate must be 0 or 1");
         if (!fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format not uploaded");
         need(fmt->v.M == 0 || O == 0 || dC, "null C");
         need(fmt->v.num_groups() == 0 || O == 0 || dB, "null B");
         need_device();
-        run_timed((hipStream_t)stream, ms, [&] {
-            return vcsr::launch_vcsr_stream(fmt->v, fmt->dev, dB, O, tileK, dC,
-                                            (hipStream_t)stream);
+        if (kernel == VCSR_KERNEL_AUTO) kernel = VCSR_KERNEL_ROW;
+        hipStream_t st = (hipStream_t)stream;
+        DeviceFmt& d = const_cast<vcsr_fmt*>(fmt)->dev;
+        if (kernel == VCSR_KERNEL_ROW && d.n_partials > 0 && d.partials_cols < O) {
+            // Scratch for the chunk sums of split rows, kept with the format.
+            hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+            if (d.partials) hip_check(hipFree(d.partials), "hipFree");
+            d.partials = nullptr;
+            d.partials_cols = 0;
+            const size_t bytes = (size_t)d.n_partials * (size_t)O * sizeof(float);
+            hipError_t e = hipMalloc((void**)&d.partials, bytes);
+            if (e == hipErrorOutOfMemory) throw vcsr::Error(VCSR_ENOMEM, "device allocation failed");
+            hip_check(e, "hipMalloc partials");
+            d.partials_cols = O;
+        }
+        const size_t bytesC = (size_t)fmt->v.M * (size_t)O * sizeof(float);
+        run_timed(st, ms, [&]() -> hipError_t {
+            if (kernel == VCSR_KERNEL_ROW)
+                return vcsr::launch_vcsr_rowmajor(fmt->v, d, dB, O, dC, accumulate, st);
+            if (!accumulate && bytesC > 0) {
+                hipError_t e = hipMemsetAsync(dC, 0, bytesC, st);
+                if (e != hipSuccess) return e;
+            }
+            if (kernel == VCSR_KERNEL_SEGMENT)
+                return vcsr::launch_vcsr_stream(fmt->v, d, dB, O, tileK, dC, st);
+            return vcsr::launch_vcsr_mfma(fmt->v, d, dB, O, tileK, dC, st);
         });
     });
 }
 
+int spmm_vcsr(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK, float* dC,
+              void* stream, float* ms) {
+    return spmm_vcsr_ex(fmt, dB, O, tileK, dC, stream, ms, VCSR_KERNEL_AUTO, 1);
+}
+
 int spmm_vcsr_mfma(const vcsr_fmt* fmt, const float* dB, int32_t O, float* dC, void* stream,
                    float* ms) {
-    return guarded([&] {
-        need(fmt != nullptr, "null format");
-        need(O >= 0, "negative O");
-        if (!fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format not uploaded");
-        need(fmt->v.M == 0 || O == 0 || dC, "null C");
-        need(fmt->v.num_groups() == 0 || O == 0 || dB, "null B");
-        need_device();
-        run_timed((hipStream_t)stream, ms, [&] {
-            return vcsr::launch_vcsr_mfma(fmt->v, fmt->dev, dB, O, 0, dC, (hipStream_t)stream);
-        });
-    });
+    return spmm_vcsr_ex(fmt, dB, O, 0, dC, stream, ms, VCSR_KERNEL_MFMA, 1);
 }
 
 int vcsr_device_count(int32_t* n) {

@@ -23,6 +23,21 @@ struct DeviceFmt {
     int32_t* items = nullptr;           // 2*n_items: [first group, end group) per work item
     int32_t n_items = 0;
     int32_t max_depth = 0;
+    // Row-stationary view of the same slots (the inverse of group_rows):
+    // for every (group, active lane) pair, {first slot, segment base column,
+    // entry count, row}, ordered by row and, within a row, by segment.
+    int32_t* pair_rec = nullptr;        // 4*n_pairs
+    int64_t n_pairs = 0;
+    // Row work items {row, first pair, end pair, partial index or -1}: a row
+    // with more pairs than one wave should take is split into chunks whose
+    // partial sums a second kernel adds up.
+    int32_t* row_items = nullptr;       // 4*n_row_items
+    int32_t n_row_items = 0;
+    int32_t n_partials = 0;             // chunks of split rows
+    int32_t* split_rows = nullptr;      // 3*n_split: {row, first partial, partial count}
+    int32_t n_split = 0;
+    float* partials = nullptr;          // n_partials * partials_cols floats, grown on demand
+    int64_t partials_cols = 0;
 };
 
 struct vcsr_coo {
