@@ -1,0 +1,104 @@
+"""The C ABI library and the CLI without a GPU: the library loads, exports
+every function include/vcsr_spmm.h declares, refuses GPU work cleanly when no
+GPU is visible, and the CLI keeps the reference's flag surface and output
+line format (src/main.cpp:68-90; reports/a100/*_vcsr_*.txt)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "vcsr_spmm.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_expected_api():
+    names = declared_functions()
+    for n in ("vcsr_build", "vcsr_fmt_arrays", "vcsr_fmt_upload", "vcsr_fmt_free",
+              "spmm_csr_naive", "spmm_vcsr", "spmm_vcsr_mfma", "spmm_csr_cpu", "vcsr_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(vs):
+    lib = ctypes.CDLL(vs.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(vs.EXPORTS) == declared_functions()
+
+
+def test_header_compiles_as_c(tmp_path):
+    src = tmp_path / "t.c"
+    src.write_text('#include "vcsr_spmm.h"\nint main(void){return VCSR_OK;}\n')
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                        "-c", str(src), "-o", str(tmp_path / "t.o")], capture_output=True)
+    assert r.returncode == 0, r.stderr.decode()
+
+
+def test_gpu_entry_points_without_gpu(vs):
+    if vs.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(vs.VcsrError) as e:
+        vs.DeviceArray((4,), np.float32)
+    assert e.value.code == vs.VCSR_EDEVICE
+    fmt = vs.csr_to_vcsr_seg(vs.coo_to_csr(vs.generate_coo(1, 0)), 4, 64)
+    with pytest.raises(vs.VcsrError) as e:
+        fmt.upload()
+    assert e.value.code == vs.VCSR_EDEVICE
+    lib = vs.load_library()
+    rc = lib.spmm_vcsr(fmt._h, None, 8, 64, None, None, None)
+    assert rc == vs.VCSR_ESTATE  # not uploaded: refused before any device work
+    rc = lib.spmm_csr_naive(4, None, None, None, None, 8, None, None, None)
+    assert rc == vs.VCSR_EINVAL
+
+
+def run_cli(vs, *args):
+    return subprocess.run([vs.CLI_PATH, *args], capture_output=True, text=True, timeout=300)
+
+
+def test_cli_usage_errors(vs):
+    assert run_cli(vs).returncode == 1                       # no --mtx / --gen
+    assert run_cli(vs, "--bogus").returncode == 1            # unknown option
+    assert run_cli(vs, "--gen", "cfg1", "--algo", "nope").returncode == 1
+    r = run_cli(vs, "--gen", "cfg1", "--algo", "cusparse")
+    assert r.returncode == 1 and "not part of this build" in r.stdout
+
+
+def test_cli_cpu_line_format(vs, tmp_path):
+    """The last line carries the tokens the reference's bench parsers take:
+    the number before "ms" and before "GFLOP/s" (run_h100_bench.slurm:60-61)."""
+    r = run_cli(vs, "--gen", "cfg1", "--O", "32", "--algo", "cpu", "--repeat", "2")
+    assert r.returncode == 0, r.stderr
+    last = r.stdout.strip().splitlines()[-1]
+    tok = last.split()
+    ms = float(tok[tok.index("ms") - 1])
+    gf = float(tok[tok.index("GFLOP/s") - 1])
+    assert ms > 0 and gf > 0
+    assert "Matrix: 4096 x 4096, nnz=65536" in r.stdout
+
+
+def test_cli_reads_mtx(vs, tmp_path):
+    p = tmp_path / "a.mtx"
+    p.write_text("%%MatrixMarket matrix coordinate real general\n3 3 4\n1 1 1\n2 2 2\n3 3 3\n1 3 4\n")
+    r = run_cli(vs, "--mtx", str(p), "--O", "8", "--algo", "cpu")
+    assert r.returncode == 0, r.stderr
+    assert "Matrix: 3 x 3, nnz=4" in r.stdout
+    r = run_cli(vs, "--mtx", str(tmp_path / "missing.mtx"), "--algo", "cpu")
+    assert r.returncode != 0 and "Failed to open MTX" in r.stderr
+
+
+def test_cli_gpu_algo_without_gpu(vs):
+    if vs.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    r = run_cli(vs, "--gen", "cfg1", "--algo", "vcsr")
+    assert r.returncode == 2 and "no GPU" in r.stderr

@@ -1,0 +1,264 @@
+"""Product host library (through its C ABI) against the pinned oracle and the
+reference-made golden fixtures: Matrix Market reader, COO->CSR, the three
+VCSR builders (bit-exact, any thread count), the synthetic generators, the
+CPU SpMM, and the error behaviour of each entry point."""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+
+from conftest import ROOT, random_csr
+
+ARRAYS = ("group_ptr", "group_depth", "group_seg_base", "group_rows", "lcol", "val")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with open(os.path.join(ROOT, "tests", "golden", "vcsr_golden.json")) as f:
+        return json.load(f)
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def product_csr(vs, M, N, rows, cols, vals):
+    return vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
+
+
+# ------------------------------------------------------------------ builders
+@settings(max_examples=60, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(seed=st.integers(0, 2**31 - 1), segw=st.integers(1, 20), bundle=st.integers(1, 80),
+       layout=st.sampled_from([0, 1, 2]), threads=st.sampled_from([1, 3, 0]))
+def test_builders_match_oracle(vs, orc, seed, segw, bundle, layout, threads):
+    rng = np.random.default_rng(seed)
+    M, N = int(rng.integers(0, 90)), int(rng.integers(1, 70))
+    rows, cols, vals = random_csr(rng, M, N, density=float(rng.uniform(0.0, 0.4)),
+                                  dup_rate=float(rng.choice([0.0, 0.3])), empty_rows=0.2)
+    csr = product_csr(vs, M, N, rows, cols, vals)
+    fmt = vs.build_vcsr(csr, segw, bundle, layout, threads)
+    got = fmt.arrays()
+    want = orc.build(M, N, csr.row_ptr, csr.col, csr.val, segw, bundle, layout)
+    for k in ARRAYS + ("segment_group_start",):
+        assert np.array_equal(got[k], want[k]), k
+    assert fmt.num_groups == want["num_groups"] and fmt.num_slots == want["num_slots"]
+
+
+def test_builders_thread_count_invariant(vs):
+    csr = vs.coo_to_csr(vs.generate_coo(1, 3))
+    for layout in (0, 1, 2):
+        ref = vs.build_vcsr(csr, 4, 64, layout, 1).arrays()
+        for t in (2, 7, 0):
+            got = vs.build_vcsr(csr, 4, 64, layout, t).arrays()
+            for k in ref:
+                assert np.array_equal(ref[k], got[k]), (layout, t, k)
+
+
+def test_builders_golden_tiny(vs, golden):
+    for name, case in golden["tiny"].items():
+        csr = vs.Csr.from_arrays(case["M"], case["N"], case["row_ptr"], case["col"], case["val"])
+        for key, fx in case["fmt"].items():
+            got = vs.build_vcsr(csr, fx["segw"], fx["bundle"], fx["layout"]).arrays()
+            for k in ARRAYS:
+                want = np.asarray(fx[k], np.float32 if k == "val" else np.int32)
+                assert np.array_equal(got[k], want), f"{name}/{key}/{k}"
+
+
+def test_builders_golden_large(vs, golden):
+    for cfg_name, entry in golden["large"].items():
+        csr = vs.coo_to_csr(vs.generate_coo(int(cfg_name[3:]), entry["seed"]))
+        assert sha(csr.row_ptr) == entry["csr_sha256"]["row_ptr"]
+        assert sha(csr.col) == entry["csr_sha256"]["col"]
+        assert sha(csr.val) == entry["csr_sha256"]["val"]
+        for key, fx in entry["fmt"].items():
+            got = vs.build_vcsr(csr, fx["segw"], fx["bundle"], fx["layout"]).arrays()
+            for k in ARRAYS:
+                assert sha(got[k]) == fx["sha256"][k], f"{cfg_name}/{key}/{k}"
+
+
+def test_tc_forces_16x16(vs):
+    csr = vs.coo_to_csr(vs.generate_coo(1, 0))
+    f = vs.build_vcsr(csr, 3, 7, vs.LAYOUT_TC)
+    assert (f.segw, f.bundle) == (16, 16)
+
+
+# --------------------------------------------------------------- COO -> CSR
+@settings(max_examples=40, deadline=None)
+@given(seed=st.integers(0, 2**31 - 1))
+def test_coo_to_csr_matches_oracle(vs, orc, seed):
+    rng = np.random.default_rng(seed)
+    M, N = int(rng.integers(0, 60)), int(rng.integers(1, 40))
+    n = int(rng.integers(0, 300))
+    rows = rng.integers(0, max(M, 1), n).astype(np.int32) if M else np.zeros(0, np.int32)
+    cols = rng.integers(0, N, len(rows)).astype(np.int32)
+    vals = rng.normal(size=len(rows)).astype(np.float32)
+    csr = product_csr(vs, M, N, rows, cols, vals)
+    rp, col, val = orc.coo_to_csr(M, N, rows, cols, vals)
+    assert np.array_equal(csr.row_ptr, rp)
+    assert np.array_equal(csr.col, col)
+    assert np.array_equal(csr.val, val)
+
+
+def test_coo_to_csr_golden(vs, golden):
+    for name, case in golden["csr"].items():
+        csr = product_csr(vs, case["M"], case["N"], case["rows"], case["cols"], case["vals"])
+        assert csr.row_ptr.tolist() == case["row_ptr"], name
+        assert csr.col.tolist() == case["col"], name
+        assert np.array_equal(csr.val, np.asarray(case["val"], np.float32)), name
+
+
+# ------------------------------------------------------------- Matrix Market
+def test_mtx_golden(vs, golden, tmp_path):
+    for name, case in golden["mtx"].items():
+        p = tmp_path / f"{name}.mtx"
+        p.write_text(case["text"])
+        coo = vs.read_matrix_market_coo(str(p))
+        assert (coo.M, coo.N) == (case["M"], case["N"])
+        assert coo.rows.tolist() == case["rows"] and coo.cols.tolist() == case["cols"]
+        assert np.array_equal(coo.vals, np.asarray(case["vals"], np.float32)), name
+
+
+def test_mtx_matches_oracle_random(vs, orc, tmp_path):
+    rng = np.random.default_rng(5)
+    for i in range(5):
+        M, N, n = 30, 20, 100
+        r = rng.integers(1, M + 1, n)
+        c = rng.integers(1, N + 1, n)
+        v = rng.normal(size=n) * 10.0 ** rng.integers(-8, 8, n)
+        lines = ["%%MatrixMarket matrix coordinate real general", "% c", f"{M} {N} {n}"]
+        lines += [f"{a} {b} {float(x)!r}" for a, b, x in zip(r, c, v)]
+        p = tmp_path / f"r{i}.mtx"
+        p.write_text("\n".join(lines) + "\n")
+        coo = vs.read_matrix_market_coo(str(p))
+        o = orc.read_mtx(str(p))
+        assert (coo.M, coo.N) == (o[0], o[1])
+        assert np.array_equal(coo.rows, o[2]) and np.array_equal(coo.cols, o[3])
+        assert np.array_equal(coo.vals, o[4])
+
+
+def test_mtx_symmetric_expansion_opt_in(vs, tmp_path):
+    p = tmp_path / "s.mtx"
+    p.write_text("%%MatrixMarket matrix coordinate real symmetric\n3 3 3\n1 1 2\n3 1 -1\n2 2 4\n")
+    plain = vs.read_matrix_market_coo(str(p))
+    assert plain.nnz == 3  # the reference does not expand (include/mmio.hpp:29)
+    full = vs.read_matrix_market_coo(str(p), expand_symmetric=True)
+    assert full.nnz == 4
+    trip = sorted(zip(full.rows.tolist(), full.cols.tolist(), full.vals.tolist()))
+    assert trip == [(0, 0, 2.0), (0, 2, -1.0), (1, 1, 4.0), (2, 0, -1.0)]
+
+
+@pytest.mark.parametrize("text,code", [
+    ("%%MatrixMarket matrix coordinate real general\n% only comments\n", 2),
+    ("", 2),
+    ("%%MatrixMarket matrix coordinate real general\n2 2 3\n1 1 1.0\n2 2\n", 2),
+    ("%%MatrixMarket matrix coordinate real general\n2 2 1\n1 x 1.0\n", 2),
+])
+def test_mtx_errors(vs, tmp_path, text, code):
+    p = tmp_path / "bad.mtx"
+    p.write_text(text)
+    with pytest.raises(vs.VcsrError) as e:
+        vs.read_matrix_market_coo(str(p))
+    assert e.value.code == code
+
+
+def test_mtx_missing_file(vs):
+    with pytest.raises(vs.VcsrError) as e:
+        vs.read_matrix_market_coo("/nonexistent/file.mtx")
+    assert e.value.code == vs.VCSR_EIO
+
+
+# ------------------------------------------------------------------- errors
+def test_error_behaviour(vs):
+    with pytest.raises(vs.VcsrError) as e:  # row out of range (csr.hpp:19)
+        vs.coo_to_csr(vs.Coo.from_arrays(2, 2, [2], [0], [1.0]))
+    assert e.value.code == vs.VCSR_ERANGE
+    with pytest.raises(vs.VcsrError) as e:  # column out of range
+        vs.coo_to_csr(vs.Coo.from_arrays(2, 2, [0], [5], [1.0]))
+    assert e.value.code == vs.VCSR_ERANGE
+    csr = vs.coo_to_csr(vs.Coo.from_arrays(3, 3, [0, 1], [0, 2], [1.0, 2.0]))
+    for segw, bundle in [(0, 4), (4, 0), (-1, 4), (4, -3)]:
+        with pytest.raises(vs.VcsrError) as e:
+            vs.build_vcsr(csr, segw, bundle, vs.LAYOUT_S)
+        assert e.value.code == vs.VCSR_EINVAL
+    with pytest.raises(vs.VcsrError):
+        vs.build_vcsr(csr, 4, 4, 7)
+    with pytest.raises(vs.VcsrError) as e:  # invalid CSR
+        vs.Csr.from_arrays(2, 2, [0, 2, 1], [0, 1], [1.0, 1.0])
+    assert e.value.code == vs.VCSR_ERANGE
+    with pytest.raises(vs.VcsrError):
+        vs.generate_coo(9, 0)
+    assert vs.load_library().vcsr_last_error() != b""
+
+
+# --------------------------------------------------------------- generators
+def test_generators_deterministic(vs):
+    a, b = vs.generate_coo(1, 42), vs.generate_coo(1, 42)
+    assert np.array_equal(a.cols, b.cols) and np.array_equal(a.vals, b.vals)
+    c = vs.generate_coo(1, 43)
+    assert not np.array_equal(a.cols, c.cols)
+    x, y = vs.gen_dense(7, 0, 100, 9), vs.gen_dense(7, 0, 100, 9)
+    assert np.array_equal(x, y)
+    assert x.min() >= -1 and x.max() < 1
+    # element i depends only on (seed, i): a prefix is the same matrix's prefix
+    assert np.array_equal(vs.gen_dense(7, 0, 50, 9), x[:50])
+    n = vs.gen_dense(3, 1, 20000, 8)
+    assert abs(n.mean()) < 0.02 and abs(n.std() - 1) < 0.02
+
+
+def test_cfg1_shape(vs):
+    coo = vs.generate_coo(1, 0)
+    assert (coo.M, coo.N, coo.nnz) == (4096, 4096, 65536)
+    cols = coo.cols.reshape(4096, 16)
+    assert all(len(set(r.tolist())) == 16 for r in cols)
+    assert coo.vals.min() >= -1 and coo.vals.max() < 1
+
+
+def test_cfg2_shape(vs):
+    csr = vs.coo_to_csr(vs.generate_coo(2, 0))
+    assert csr.M == csr.N == 62451
+    rl = np.diff(csr.row_ptr)
+    assert rl.min() >= 40 and rl.max() <= 78 and 60 <= rl.mean() <= 68
+    rows = np.repeat(np.arange(csr.M), rl)
+    assert np.abs(rows - csr.col).max() <= 3 * 333 + 2  # band
+    key = lambda r, c: r.astype(np.int64) * csr.N + c
+    fwd = dict(zip(key(rows, csr.col).tolist(), csr.val.tolist()))
+    back = [fwd[k] for k in key(csr.col, rows).tolist()]  # symmetric pattern and values
+    assert np.array_equal(np.asarray(back, np.float32), csr.val)
+    diag = csr.val[rows == csr.col]
+    offl1 = np.bincount(rows, weights=np.abs(csr.val) * (rows != csr.col), minlength=csr.M)
+    assert np.all(diag >= offl1)  # diagonally dominant
+
+
+def test_cfg3_shape(vs):
+    csr = vs.coo_to_csr(vs.generate_coo(3, 0))
+    assert csr.M == 321821
+    assert 1.7e6 <= csr.nnz <= 2.1e6
+    rl = np.diff(csr.row_ptr)
+    assert rl.min() >= 1 and rl.max() >= 5000
+    rows = np.repeat(np.arange(csr.M), rl)
+    assert np.count_nonzero(rows == csr.col) == csr.M  # full diagonal
+
+
+def test_cfg5_shape(vs):
+    csr = vs.coo_to_csr(vs.generate_coo(5, 0))
+    assert csr.M == 16384 and csr.nnz == 1024 * 51 * 256
+    rl = np.diff(csr.row_ptr)
+    assert np.all(rl == 51 * 16)
+
+
+# ------------------------------------------------------------------ CPU SpMM
+@pytest.mark.parametrize("threads", [1, 4, 0])
+def test_cpu_spmm_matches_oracle_bitwise(vs, orc, threads):
+    rng = np.random.default_rng(threads)
+    rows, cols, vals = random_csr(rng, 200, 150, density=0.05, dup_rate=0.1, empty_rows=0.1)
+    csr = product_csr(vs, 200, 150, rows, cols, vals)
+    B = vs.gen_dense(1, 0, 150, 37)
+    C = vs.spmm_csr_cpu(csr, B, threads)
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))

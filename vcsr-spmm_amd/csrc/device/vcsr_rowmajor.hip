@@ -178,24 +178,34 @@ __global__ __launch_bounds__(256) void vcsr_rowmajor_kernel(
         // 64-bit path: clamped to column 0) and never store.
         const uint32_t koff = (uint32_t)((kok || BUF) ? k : 0) * 4u;
         V acc = zero_vec(V());
-        for (int32_t i0 = 0; i0 < ninstr; i0 += U) {
+        auto load_entry = [&](int32_t t, V& b, float& a) {
+            const uint2 e = list[t];
+            a = __builtin_bit_cast(float, e.y);
+            if constexpr (BUF)
+                b = load_b<VEC, true>(rsrc, B, e.x + koff);
+            else
+                b = *reinterpret_cast<const V*>(B + (int64_t)e.x * O + koff / 4);
+        };
+        // Full blocks: every sub-group has an entry in each instruction.
+        const int32_t nfull = (total / EPI) / U * U;
+        for (int32_t i0 = 0; i0 < nfull; i0 += U) {
+            V b[U];
+            float a[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) load_entry((i0 + u) * EPI + sub, b[u], a[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u) fma_vec(acc, a[u], b[u]);
+        }
+        // Tail: fewer than U instructions, the last one possibly partial.
+        if (nfull < ninstr) {
             V b[U];
             float a[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 a[u] = 0.f;
                 b[u] = zero_vec(V());
-                if (i0 + u < ninstr) {
-                    const int32_t t = (i0 + u) * EPI + sub;
-                    if (t < total) {
-                        const uint2 e = list[t];
-                        a[u] = __builtin_bit_cast(float, e.y);
-                        if constexpr (BUF)
-                            b[u] = load_b<VEC, true>(rsrc, B, e.x + koff);
-                        else
-                            b[u] = *reinterpret_cast<const V*>(B + (int64_t)e.x * O + koff / 4);
-                    }
-                }
+                const int32_t t = (nfull + u) * EPI + sub;
+                if (t < total) load_entry(t, b[u], a[u]);
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) fma_vec(acc, a[u], b[u]);
