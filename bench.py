@@ -4,12 +4,14 @@ Workload (the headline): banded FEM-like A, 62,451^2,
 ~3.94M nnz (synthetic, seed 0), dense B 62,451 x 128 FP32 U[-1,1), VCSR
 layout S with segw=4, bundle=64, tileK=64, built and uploaded before timing.
 
-A step is one complete SpMM C = A*B on device-resident inputs: reset C (the
-VCSR kernel accumulates into C, as the reference's does) and run the
-segmented-streaming kernel.  K steps are timed between HIP events after W
-warm-up steps; `value` is 2*nnz*O*K / that time.  The kernel alone is then
-timed per launch with events on its stream (the reference's convention,
-src/kernels.cu:153-162) for `kernel_ms` and the roofline.
+A step is one complete SpMM C = A*B on device-resident inputs.  The default
+kernel (spmm_vcsr_ex, VCSR_KERNEL_AUTO = the row-stationary VCSR kernel with
+accumulate = 0) writes every element of C, so a step is one launch; the
+kernels that accumulate into C as the reference's do (--algo segment / mfma)
+get a C reset inside the step.  K steps are timed between HIP events after W
+warm-up steps; `value` is 2*nnz*O*K / that time.  `kernel_ms` is the kernel
+alone, K back-to-back launches between events on its stream (the reference
+times kernels only, src/kernels.cu:153-162); the roofline uses it.
 
 Prints ONE JSON line.  Multi-GPU runs are not part of this build.
 """
@@ -59,6 +61,22 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def measured_traffic(config, algo):
+    """HBM-side bytes per launch of the dominant kernel, from the committed
+    rocprofv3 counter summary (profiles/traffic.json): FETCH_SIZE and
+    WRITE_SIZE of the kernel, each divided by what the same counter reads
+    per byte for a device-to-device copy of known size.  None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        e = t["kernels"][f"{config}/{algo}"]
+        return (e["fetch_kib"] * 1024.0 / t["copy_fetch_factor"] +
+                e["write_kib"] * 1024.0 / t["copy_write_factor"])
+    except (OSError, KeyError, ValueError, ZeroDivisionError):
+        return None
+
+
 def cpu_baseline(orc, csr, B, seconds):
     """The oracle's single-thread FP32 CSR SpMM (reference loop order) on the
     same matrix and B, repeated until `seconds` of CPU work."""
@@ -82,6 +100,9 @@ def main():
     ap.add_argument("--tileK", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only copy a BYTES buffer device-to-device --steps times (the "
+                         "known-size kernel that scales the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -94,6 +115,20 @@ def main():
     if vs.device_count() <= 0:
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration > 0:
+        st = vs.Stream()
+        src = vs.DeviceArray((args.copy_calibration // 4,), np.float32)
+        dst = vs.DeviceArray((args.copy_calibration // 4,), np.float32)
+        src.zero(st)
+        ev0, ev1 = vs.Event(), vs.Event()
+        ev0.record(st)
+        for _ in range(args.steps):
+            dst.copy_from(src, st)
+        ev1.record(st)
+        ms = ev0.elapsed_ms(ev1) / args.steps
+        print(json.dumps({"copy_bytes": src.nbytes, "ms_per_copy": round(ms, 5),
+                          "gbs_read_plus_write": round(2 * src.nbytes / ms / 1e6, 1)}))
+        return
     from oracle import oracle as orc
 
     cfg, O, segw, bundle, tileK, layout, dist = CONFIGS[args.config]
@@ -167,11 +202,21 @@ def main():
     check = "pass" if rel <= 1e-5 else "FAIL"
     log(f"bench: sampled-row rel L2 vs oracle {rel:.2e} ({check})")
 
-    # Kernel-only duration: events around each launch on the kernel's stream.
-    kms = []
-    for _ in range(max(10, min(args.steps, 100))):
-        kms.append(kernel(timed=True))
-    kernel_ms = float(np.mean(kms))
+    # Kernel-only duration: the kernel alone, K launches back to back between
+    # two events on the stream it runs on (C is left accumulating; the
+    # timing does not depend on its contents).  Without a reset in the step
+    # this equals ms_per_step.
+    if needs_reset:
+        e0, e1 = vs.Event(), vs.Event()
+        lib.vcsr_device_sync()
+        e0.record(st)
+        for _ in range(args.steps):
+            kernel()
+        e1.record(st)
+        kernel_ms = e0.elapsed_ms(e1) / args.steps
+        lib.vcsr_device_sync()
+    else:
+        kernel_ms = total_ms / args.steps
 
     flop = 2.0 * csr.nnz * O
     ms_per_step = total_ms / args.steps
@@ -201,7 +246,8 @@ def main():
         "check": {"rel_l2_sampled_rows": rel, "result": check},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_alg": bytes_alg},
+                     "traffic": measured_traffic(args.config, args.algo),
+                     "bytes_alg": bytes_alg},
     }
     if not args.no_cpu_baseline:
         gf, reps, secs = cpu_baseline(orc, csr, B, args.cpu_seconds)

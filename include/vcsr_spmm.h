@@ -212,6 +212,8 @@ int vcsr_dev_malloc(void** ptr, size_t bytes);
 int vcsr_dev_free(void* ptr);
 int vcsr_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int vcsr_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+/* Device-to-device copy, enqueued on `stream` (not waited for). */
+int vcsr_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int vcsr_memset_d(void* dst, int32_t value, size_t bytes, void* stream);
 int vcsr_stream_create(void** stream);
 int vcsr_stream_destroy(void* stream);

@@ -43,7 +43,7 @@ EXPORTS = (
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
     "vcsr_fmt_free spmm_csr_naive spmm_vcsr spmm_vcsr_ex spmm_vcsr_mfma spmm_csr_cpu "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
-    "vcsr_memcpy_d2h vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
+    "vcsr_memcpy_d2h vcsr_memcpy_d2d vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
     "vcsr_stream_sync vcsr_device_sync vcsr_event_create vcsr_event_destroy "
     "vcsr_event_record vcsr_event_elapsed"
 ).split()
@@ -118,6 +118,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "vcsr_dev_free": (C.c_int, [P]),
         "vcsr_memcpy_h2d": (C.c_int, [P, P, C.c_size_t, P]),
         "vcsr_memcpy_d2h": (C.c_int, [P, P, C.c_size_t, P]),
+        "vcsr_memcpy_d2d": (C.c_int, [P, P, C.c_size_t, P]),
         "vcsr_memset_d": (C.c_int, [P, I32, C.c_size_t, P]),
         "vcsr_stream_create": (C.c_int, [pP]),
         "vcsr_stream_destroy": (C.c_int, [P]),
@@ -374,6 +375,11 @@ class DeviceArray:
         out = np.empty(self.shape, dtype=self.dtype)
         _check(load_library().vcsr_memcpy_d2h(_ptr(out), self.ptr, self.nbytes, _sp(stream)))
         return out
+
+    def copy_from(self, other: "DeviceArray", stream=None) -> None:
+        """Device-to-device copy of min(nbytes) bytes, enqueued on stream."""
+        n = min(self.nbytes, other.nbytes)
+        _check(load_library().vcsr_memcpy_d2d(self.ptr, other.ptr, n, _sp(stream)))
 
     def zero(self, stream=None) -> None:
         _check(load_library().vcsr_memset_d(self.ptr, 0, self.nbytes, _sp(stream)))

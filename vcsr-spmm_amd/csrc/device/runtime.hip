@@ -396,6 +396,15 @@ int vcsr_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
     });
 }
 
+int vcsr_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    return guarded([&] {
+        if (bytes == 0) return;
+        need(dst && src, "null pointer");
+        hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                  "hipMemcpyAsync d2d");
+    });
+}
+
 int vcsr_memset_d(void* dst, int32_t value, size_t bytes, void* stream) {
     return guarded([&] {
         if (bytes == 0) return;
