@@ -15,8 +15,9 @@
 // pair's slots (lcol, val) and writes each entry as (byte offset of its B
 // row, value) into the wave's LDS list at the wave-exclusive prefix sum of
 // the entry counts.
-// Phase 2: the wave streams the list in blocks, two blocks of loads in
-// flight (ping-pong register sets).  The vector memory pipe takes about 16
+// Phase 2: the wave streams the list in blocks of 16 load instructions
+// issued back to back (all full blocks unpredicated, then one predicated tail
+// block), so 16 B-row loads are in flight per wave.  The vector memory pipe takes about 16
 // cycles per load instruction whatever its width, so every instruction is a
 // 16-byte-per-lane load and, when O is small, serves several entries at
 // once (one per group of lanes).  B is read with raw buffer loads: the 32-bit
