@@ -96,7 +96,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
-    ap.add_argument("--algo", default="vcsr", choices=["vcsr", "row", "segment", "mfma", "csr"])
+    ap.add_argument("--algo", default="vcsr", choices=["vcsr", "tile", "row", "segment", "mfma", "csr"])
     ap.add_argument("--tileK", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -163,9 +163,12 @@ def main():
         fmt.upload(st)
         log(f"bench: VCSR layout={layout} groups={fmt.num_groups} slots={fmt.num_slots} "
             f"build {tb*1e3:.1f} ms upload {(time.perf_counter()-t0)*1e3:.1f} ms")
-        kern = {"vcsr": vs.KERNEL_AUTO, "row": vs.KERNEL_ROW, "segment": vs.KERNEL_SEGMENT,
-                "mfma": vs.KERNEL_MFMA}[args.algo]
-        overwrite = kern in (vs.KERNEL_AUTO, vs.KERNEL_ROW)
+        tr, tt, te = fmt.tile_info()
+        log(f"bench: row-tile view: {tt} tiles of <= {tr} rows, {te} entries "
+            f"({csr.nnz / max(te, 1):.2f} nonzeros per B-row load)")
+        kern = {"vcsr": vs.KERNEL_AUTO, "tile": vs.KERNEL_TILE, "row": vs.KERNEL_ROW,
+                "segment": vs.KERNEL_SEGMENT, "mfma": vs.KERNEL_MFMA}[args.algo]
+        overwrite = kern in (vs.KERNEL_AUTO, vs.KERNEL_TILE, vs.KERNEL_ROW)
         needs_reset = not overwrite
 
         def kernel(timed=False):

@@ -136,6 +136,15 @@ int vcsr_fmt_arrays(const vcsr_fmt* fmt, vcsr_arrays* out);
  * src/kernels.cu:139-151 and the one-time static upload of
  * src/vcsr_seg.cu:196-211.  The handle owns the device copy: no globals. */
 int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream);
+/* Tile height of the row-tile view vcsr_fmt_upload derives for the
+ * tile-stationary kernel (VCSR_KERNEL_TILE): rows = 1, 2, 4 or 8 forces it,
+ * 0 (the default) picks it from the matrix.  Only before the upload
+ * (VCSR_ESTATE after).  No reference counterpart. */
+int vcsr_fmt_set_tile_rows(vcsr_fmt* fmt, int32_t rows);
+/* The uploaded view's tile height, tile count and entry count (B-row slice
+ * loads per column tile of one SpMM; nnz for tile height 1).  No reference
+ * counterpart. */
+int vcsr_fmt_tile_info(const vcsr_fmt* fmt, int32_t* rows, int64_t* tiles, int64_t* entries);
 /* Free host and device memory (replaces destroy_vcsr_*_device,
  * src/vcsr_seg.cu:233-243). */
 void vcsr_fmt_free(vcsr_fmt* fmt);
@@ -154,9 +163,11 @@ int spmm_csr_naive(int32_t M, const int32_t* d_rowptr, const int32_t* d_col,
                    const float* d_val, const float* dB, int32_t O, float* dC,
                    void* stream, float* ms);
 
-/* C += A*B with the VCSR segmented-streaming kernel on an uploaded format
- * (any layout).  C is accumulated into: zero it first, as main.cpp:126-143
- * does.  tileK is the width of the C/B column tile each wavefront owns.
+/* C += A*B over an uploaded VCSR format (any layout) with the fastest kernel
+ * (VCSR_KERNEL_AUTO).  C is accumulated into: zero it first, as
+ * main.cpp:126-143 does.  tileK is the C/B column tile of the segment-major
+ * kernels (spmm_vcsr_ex); the row- and tile-stationary kernels size their
+ * column tiles from O.
  * Replaces run_vcsr_spmm_gpu (src/kernels.cu:120-167),
  * run_vcsr_seg_spmm_gpu (src/vcsr_seg.cu:191-231) and
  * run_vcsr_opt_spmm_gpu (src/vcsr_opt.cu:243-285). */
@@ -165,22 +176,26 @@ int spmm_vcsr(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
 
 /* Kernel selection of spmm_vcsr_ex (all consume the same uploaded format). */
 enum {
-    VCSR_KERNEL_AUTO = 0,    /* the fastest kernel for the format (currently ROW) */
+    VCSR_KERNEL_AUTO = 0,    /* the fastest kernel for the format (currently TILE) */
     VCSR_KERNEL_SEGMENT = 1, /* segment-major streaming on the vector ALUs, B tile
                                 in LDS, C flushed with FP32 atomics per group   */
     VCSR_KERNEL_MFMA = 2,    /* segment-major, group collapsed to a dense tile on
                                 FP32 MFMA, C flushed with FP32 atomics          */
-    VCSR_KERNEL_ROW = 3      /* row-stationary: one wavefront per C row walks the
+    VCSR_KERNEL_ROW = 3,     /* row-stationary: one wavefront per C row walks the
                                 row's (group, lane) slots; C written once, no
                                 atomics                                         */
+    VCSR_KERNEL_TILE = 4     /* tile-stationary: runs of up to 8 consecutive rows
+                                sharing columns are walked together, each B row
+                                slice loaded once per tile; C written once     */
 };
 
 /* spmm_vcsr with an explicit kernel and C semantics: accumulate = 1 gives
  * C += A*B (the reference's semantics), accumulate = 0 gives C = A*B without
- * a separate reset (the ROW kernel writes every row once; the segment-major
- * kernels clear C on the stream first).  tileK applies to the segment-major
- * kernels.  Calls on one format must not overlap in time: the ROW kernel keeps
- * a scratch buffer for the partial sums of very long rows in the format.
+ * a separate reset (the ROW and TILE kernels write every row once; the
+ * segment-major kernels clear C on the stream first).  tileK applies to the
+ * segment-major kernels.  Calls on one format must not overlap in time: the
+ * ROW and TILE kernels keep a scratch buffer in the format for the partial
+ * sums of very long rows / tiles.
  * No reference counterpart (the reference selects kernels by --algo in
  * src/main.cpp:119-163 and always accumulates). */
 int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,

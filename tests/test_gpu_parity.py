@@ -30,7 +30,7 @@ def _device_csr(vs, csr, st):
             vs.DeviceArray.from_numpy(csr.val, st))
 
 
-def _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=64):
+def _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=64, tile_rows=0):
     """Runs one kernel through the C ABI and returns C as numpy."""
     M, O = csr.M, B.shape[1]
     dB = vs.DeviceArray.from_numpy(B, st)
@@ -41,6 +41,7 @@ def _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=64):
         ms = vs.run_csr_spmm_gpu(M, rp, col, val, dB, O, dC, st, timed=True)
     else:
         fmt = vs.build_vcsr(csr, segw, bundle, layout)
+        fmt.set_tile_rows(tile_rows)
         fmt.upload(st)
         if kind == "vcsr":
             ms = vs.run_vcsr_spmm_gpu(fmt, dB, O, tileK, dC, st, timed=True)
@@ -50,6 +51,9 @@ def _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=64):
         elif kind == "row":
             ms = vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, tileK, dC, st, timed=True,
                                          kernel=vs.KERNEL_ROW)
+        elif kind == "tile":
+            ms = vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, tileK, dC, st, timed=True,
+                                         kernel=vs.KERNEL_TILE)
         else:
             ms = vs.run_vcsr_tc_spmm_gpu(fmt, dB, O, dC, st, timed=True)
     assert ms is not None and ms >= 0.0
@@ -85,7 +89,8 @@ def test_csr_naive_bit_exact_cfg1(gpu, orc, st):
 
 # ---------------------------------------------------- VCSR kernels, small
 KERNELS = [("vcsr", 1), ("vcsr", 0), ("mfma", 1), ("mfma", 0), ("mfma", 2), ("vcsr", 2),
-           ("segment", 1), ("segment", 0), ("segment", 2), ("row", 1), ("row", 0), ("row", 2)]
+           ("segment", 1), ("segment", 0), ("segment", 2), ("row", 1), ("row", 0), ("row", 2),
+           ("tile", 1), ("tile", 0), ("tile", 2)]
 
 
 @pytest.mark.parametrize("kind,layout", KERNELS)
@@ -102,7 +107,7 @@ def test_vcsr_kernels_random(gpu, orc, st, kind, layout, O):
     assert_within_tolerance(C, ref32.astype(np.float64), csr.row_ptr, csr.val, B, "vs f32")
 
 
-@pytest.mark.parametrize("kind", ["segment", "mfma", "row"])
+@pytest.mark.parametrize("kind", ["segment", "mfma", "row", "tile"])
 @pytest.mark.parametrize("segw,bundle,tileK", [(1, 64, 32), (3, 64, 100), (8, 64, 128),
                                                (16, 32, 64), (5, 20, 32), (20, 64, 256),
                                                (4, 128, 64), (4, 1, 32), (33, 16, 64)])
@@ -187,7 +192,7 @@ def _colsum_check(csr, B, C):
 
 @pytest.mark.parametrize("cfg,O,segw,tileK,layout", [(2, 128, 4, 64, 1), (3, 128, 4, 128, 1),
                                                      (2, 8, 4, 64, 1), (5, 64, 16, 64, 2)])
-@pytest.mark.parametrize("kind", ["segment", "mfma", "row"])
+@pytest.mark.parametrize("kind", ["segment", "mfma", "row", "tile"])
 def test_full_size_configs(gpu, orc, st, cfg, O, segw, tileK, layout, kind):
     vs = gpu
     csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
@@ -217,7 +222,7 @@ def _ex(vs, fmt, B, C0, st, kernel, accumulate, tileK=64):
     return dC.numpy(st)
 
 
-@pytest.mark.parametrize("kernel", [1, 2, 3])
+@pytest.mark.parametrize("kernel", [1, 2, 3, 4])
 @pytest.mark.parametrize("O", [5, 64, 130, 256, 300])
 def test_accumulate_and_overwrite(gpu, orc, st, kernel, O):
     """accumulate=1 adds A*B to the C it is given; accumulate=0 replaces it."""
@@ -235,8 +240,9 @@ def test_accumulate_and_overwrite(gpu, orc, st, kernel, O):
     assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, "overwrite")
 
 
+@pytest.mark.parametrize("kernel", [3, 4])
 @pytest.mark.parametrize("accumulate", [True, False])
-def test_row_kernel_split_rows(gpu, orc, st, accumulate):
+def test_row_kernel_split_rows(gpu, orc, st, accumulate, kernel):
     """Rows with more (row, segment) pairs than one wave takes are split into
     chunks and reduced by a second kernel; run it twice (scratch reuse) and
     with a wider O (scratch growth)."""
@@ -256,18 +262,105 @@ def test_row_kernel_split_rows(gpu, orc, st, accumulate):
         B = vs.gen_dense(O, 0, N, O)
         C0 = np.ones((M, O), np.float32)
         ref64 = orc.spmm_f64(M, csr.row_ptr, csr.col, csr.val, B)
-        got = _ex(vs, fmt, B, C0, st, vs.KERNEL_ROW, accumulate)
+        got = _ex(vs, fmt, B, C0, st, kernel, accumulate)
         if accumulate:
             got = got - C0
         assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"split O={O}")
 
 
+@pytest.mark.parametrize("kind", ["row", "tile"])
 @pytest.mark.parametrize("cfg,O,layout", [(3, 128, 1), (4, 256, 1), (5, 512, 2)])
-def test_full_size_row_kernel(gpu, orc, st, cfg, O, layout):
+def test_full_size_row_kernel(gpu, orc, st, cfg, O, layout, kind):
     vs = gpu
     csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
     B = vs.gen_dense(cfg, 1 if cfg == 5 else 0, csr.N, O)
     segw, bundle = (16, 16) if layout == 2 else (4, 64)
-    C = _run(vs, "row", csr, B, st, layout=layout, segw=segw, bundle=bundle, tileK=128)
+    C = _run(vs, kind, csr, B, st, layout=layout, segw=segw, bundle=bundle, tileK=128)
     _rowsample_check(vs, orc, csr, B, C, 1500, cfg)
     _colsum_check(csr, B, C)
+
+
+# ------------------------------------------------------ tile-stationary kernel
+def _block_csr(vs, rng, nbr, bh, N, blocks_per_row, bw, keep):
+    """Block-structured matrix: nbr block rows of height bh, each with
+    `blocks_per_row` bh x bw blocks at random block columns; every entry is
+    kept with probability `keep`, so rows of a block row share most but not
+    all of their columns."""
+    rows, cols = [], []
+    nbc = max(1, N // bw)
+    for br in range(nbr):
+        for bc in rng.choice(nbc, size=min(blocks_per_row, nbc), replace=False):
+            rr, cc = np.meshgrid(np.arange(bh) + br * bh, np.arange(bw) + bc * bw, indexing="ij")
+            m = rng.random(rr.shape) < keep
+            rows.append(rr[m]); cols.append(cc[m])
+    rows = np.concatenate(rows).astype(np.int32)
+    cols = np.concatenate(cols).astype(np.int32)
+    vals = rng.uniform(-1, 1, rows.size).astype(np.float32)
+    return vs.coo_to_csr(vs.Coo.from_arrays(nbr * bh, N, rows, cols, vals))
+
+
+@pytest.mark.parametrize("bh,tile_rows", [(2, 0), (3, 0), (4, 0), (8, 0), (16, 0), (3, 1), (3, 2),
+                                          (3, 8), (5, 4)])
+@pytest.mark.parametrize("O", [1, 8, 33, 128, 200, 520])
+def test_tile_kernel_block_rows(gpu, orc, st, bh, tile_rows, O):
+    vs = gpu
+    rng = np.random.default_rng(bh * 100 + tile_rows * 10 + O)
+    csr = _block_csr(vs, rng, 37, bh, 300, 7, 3, 0.8)
+    B = vs.gen_dense(bh + O, 0, csr.N, O)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.set_tile_rows(tile_rows)
+    fmt.upload(st)
+    R, tiles, entries = fmt.tile_info()
+    if tile_rows:
+        assert R == tile_rows
+    elif bh >= 2:
+        assert R >= 2, "block rows should be tiled"
+    assert entries < csr.nnz or R == 1
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    C0 = rng.uniform(-1, 1, size=(csr.M, O)).astype(np.float32)
+    for accumulate in (False, True):
+        got = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate)
+        if accumulate:
+            got = got - C0
+        assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"bh{bh} R{R} O{O}")
+
+
+@pytest.mark.parametrize("tile_rows", [1, 4, 8])
+def test_tile_kernel_split_tiles(gpu, orc, st, tile_rows):
+    """Block rows wider than one work item: tiles are cut into pieces whose
+    partial sums a second kernel adds; wider O grows the scratch."""
+    vs = gpu
+    rng = np.random.default_rng(tile_rows)
+    csr = _block_csr(vs, rng, 6, 8, 4096, 600, 4, 0.9)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.set_tile_rows(tile_rows)
+    fmt.upload(st)
+    for O in (64, 64, 260):
+        B = vs.gen_dense(O, 0, csr.N, O)
+        ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+        got = _ex(vs, fmt, B, np.zeros((csr.M, O), np.float32), st, vs.KERNEL_TILE, False)
+        assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"R{tile_rows} O{O}")
+
+
+@pytest.mark.parametrize("kind", ["csr", "segment", "row", "tile"])
+def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind):
+    """Inf and NaN in B reach exactly the C entries whose rows have a nonzero
+    in that B row (an absent entry contributes nothing, not 0 * inf).  The
+    MFMA kernel is left out: it multiplies every group as a dense tile, so a
+    non-finite B value reaches every row of the groups of its segment, as
+    with the reference's tensor-core kernel."""
+    vs = gpu
+    rng = np.random.default_rng(11)
+    csr = _block_csr(vs, rng, 20, 4, 120, 5, 3, 0.6)
+    O = 36
+    B = vs.gen_dense(4, 0, csr.N, O)
+    B[5, 3] = np.inf
+    B[17, :] = np.nan
+    B[40, 7] = -np.inf
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    C = _run(vs, kind, csr, B, st, tile_rows=4)
+    assert np.array_equal(np.isnan(C), np.isnan(ref)), kind
+    assert np.array_equal(np.isposinf(C), np.isposinf(ref)), kind
+    assert np.array_equal(np.isneginf(C), np.isneginf(ref)), kind
+    fin = np.isfinite(ref)
+    assert np.allclose(C[fin], ref[fin], rtol=1e-5, atol=1e-4)

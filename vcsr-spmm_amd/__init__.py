@@ -34,14 +34,14 @@ CLI_PATH = os.path.join(_HERE, "bin", "spmm_vcsr")
 
 VCSR_OK, VCSR_EINVAL, VCSR_EIO, VCSR_ENOMEM, VCSR_EDEVICE, VCSR_ERANGE, VCSR_ESTATE = range(7)
 LAYOUT_H, LAYOUT_S, LAYOUT_TC = 0, 1, 2
-KERNEL_AUTO, KERNEL_SEGMENT, KERNEL_MFMA, KERNEL_ROW = 0, 1, 2, 3
+KERNEL_AUTO, KERNEL_SEGMENT, KERNEL_MFMA, KERNEL_ROW, KERNEL_TILE = 0, 1, 2, 3, 4
 
 # Every symbol include/vcsr_spmm.h declares (checked by the CPU test suite).
 EXPORTS = (
     "vcsr_last_error vcsr_version vcsr_mtx_read vcsr_coo_create vcsr_coo_view_get "
     "vcsr_coo_free vcsr_gen_coo vcsr_gen_dense vcsr_coo_to_csr vcsr_csr_create "
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
-    "vcsr_fmt_free spmm_csr_naive spmm_vcsr spmm_vcsr_ex spmm_vcsr_mfma spmm_csr_cpu "
+    "vcsr_fmt_set_tile_rows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_vcsr spmm_vcsr_ex spmm_vcsr_mfma spmm_csr_cpu "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
     "vcsr_memcpy_d2h vcsr_memcpy_d2d vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
     "vcsr_stream_sync vcsr_device_sync vcsr_event_create vcsr_event_destroy "
@@ -106,6 +106,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "vcsr_build": (C.c_int, [P, I32, I32, I32, I32, pP]),
         "vcsr_fmt_arrays": (C.c_int, [P, C.POINTER(_Arrays)]),
         "vcsr_fmt_upload": (C.c_int, [P, P]),
+        "vcsr_fmt_set_tile_rows": (C.c_int, [P, I32]),
+        "vcsr_fmt_tile_info": (C.c_int, [P, pI, C.POINTER(I64), C.POINTER(I64)]),
         "vcsr_fmt_free": (None, [P]),
         "spmm_csr_naive": (C.c_int, [I32, P, P, P, P, I32, P, P, pF]),
         "spmm_vcsr": (C.c_int, [P, P, I32, I32, P, P, pF]),
@@ -272,6 +274,16 @@ class Vcsr:
 
     def upload(self, stream: "Stream | None" = None) -> None:
         _check(load_library().vcsr_fmt_upload(self._h, _sp(stream)))
+
+    def set_tile_rows(self, rows: int) -> None:
+        """Tile height of the row-tile view (0 = automatic); before upload()."""
+        _check(load_library().vcsr_fmt_set_tile_rows(self._h, rows))
+
+    def tile_info(self) -> tuple[int, int, int]:
+        """(tile height, tiles, entries) of the uploaded row-tile view."""
+        r, t, e = C.c_int32(), C.c_int64(), C.c_int64()
+        _check(load_library().vcsr_fmt_tile_info(self._h, C.byref(r), C.byref(t), C.byref(e)))
+        return r.value, t.value, e.value
 
 
 def build_vcsr(csr: Csr, segw: int, bundle: int, layout: int, nthreads: int = 0) -> Vcsr:

@@ -208,6 +208,26 @@ int vcsr_fmt_arrays(const vcsr_fmt* fmt, vcsr_arrays* out) {
     });
 }
 
+int vcsr_fmt_set_tile_rows(vcsr_fmt* fmt, int32_t rows) {
+    return guarded([&] {
+        need(fmt != nullptr, "null format");
+        need(rows == 0 || rows == 1 || rows == 2 || rows == 4 || rows == 8,
+             "tile rows must be 0, 1, 2, 4 or 8");
+        if (fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format already uploaded");
+        fmt->tile_rows = rows;
+    });
+}
+
+int vcsr_fmt_tile_info(const vcsr_fmt* fmt, int32_t* rows, int64_t* tiles, int64_t* entries) {
+    return guarded([&] {
+        need(fmt != nullptr, "null format");
+        if (!fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format not uploaded");
+        if (rows) *rows = fmt->dev.tv_R;
+        if (tiles) *tiles = fmt->tv_tiles;
+        if (entries) *entries = fmt->dev.tv_n_entries;
+    });
+}
+
 void vcsr_fmt_free(vcsr_fmt* fmt) {
     if (!fmt) return;
     vcsr::free_device_fmt(fmt->dev);

@@ -33,6 +33,12 @@ int mfma_col_blocks(int32_t tileK, int32_t O);
 hipError_t launch_vcsr_rowmajor(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                                 float* C, int32_t accumulate, hipStream_t st);
 
+// vcsr_tile.hip: tile-stationary traversal of the VCSR slots through the
+// row-tile view; C = A*B (accumulate = 0) or C += A*B (accumulate = 1).
+// Needs d.partials sized for O when the view has split tiles.
+hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                            float* C, int32_t accumulate, hipStream_t st);
+
 // A row-stationary work item covers at most this many (group, lane) pair
 // records (one per lane) and entries (the wave's LDS list); longer rows are
 // split into chunks whose partial sums a second kernel adds.

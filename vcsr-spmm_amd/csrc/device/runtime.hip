@@ -10,6 +10,7 @@
 
 #include "../../../include/vcsr_spmm.h"
 #include "../fmt_internal.hpp"
+#include "../host/tile_view.hpp"
 #include "launch.hpp"
 
 namespace {
@@ -208,7 +209,8 @@ void free_device_fmt(DeviceFmt& d) {
     for (void* p : {(void*)d.group_ptr, (void*)d.group_depth, (void*)d.group_seg_base,
                     (void*)d.group_rows, (void*)d.group_nact, (void*)d.lcol, (void*)d.val,
                     (void*)d.items, (void*)d.pair_rec, (void*)d.row_items, (void*)d.split_rows,
-                    (void*)d.partials})
+                    (void*)d.tv_chunks, (void*)d.tv_pieces, (void*)d.tv_brow, (void*)d.tv_slot,
+                    (void*)d.tv_split, (void*)d.partials})
         if (p) (void)hipFree(p);
     if (d.device >= 0 && d.device != cur && cur >= 0) (void)hipSetDevice(cur);
     d = DeviceFmt();
@@ -239,6 +241,7 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
         }
         std::vector<int32_t> items = make_items(v, 256);
         RowView rv = make_row_view(v, nact);
+        const vcsr::TileView tv = vcsr::make_tile_view(v, fmt->tile_rows, 0);
         DeviceFmt d;
         hip_check(hipGetDevice(&d.device), "hipGetDevice");
         try {
@@ -260,6 +263,16 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.split_rows = upload_array(rv.split_rows, st, "upload split rows");
             d.n_split = (int32_t)(rv.split_rows.size() / 3);
             d.n_partials = rv.n_partials;
+            d.tv_R = tv.R;
+            d.tv_chunks = upload_array(tv.chunks, st, "upload tile chunks");
+            d.tv_n_chunks = (int32_t)(tv.chunks.size() / 4);
+            d.tv_pieces = upload_array(tv.pieces, st, "upload tile pieces");
+            d.tv_brow = upload_array(tv.brow, st, "upload tile entries");
+            d.tv_slot = upload_array(tv.slot, st, "upload tile slots");
+            d.tv_n_entries = tv.n_entries();
+            d.tv_split = upload_array(tv.split, st, "upload split tiles");
+            d.tv_n_split = (int32_t)(tv.split.size() / 4);
+            d.tv_partial_rows = tv.n_partial_rows;
             // The host vectors above must outlive the copies.
             hip_check(hipStreamSynchronize(st), "upload sync");
         } catch (...) {
@@ -267,6 +280,7 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             throw;
         }
         fmt->dev = d;
+        fmt->tv_tiles = tv.n_tiles;
     });
 }
 
@@ -289,22 +303,23 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
     return guarded([&] {
         need(fmt != nullptr, "null format");
         need(O >= 0, "negative O");
-        need(kernel >= VCSR_KERNEL_AUTO && kernel <= VCSR_KERNEL_ROW, "unknown kernel");
+        need(kernel >= VCSR_KERNEL_AUTO && kernel <= VCSR_KERNEL_TILE, "unknown kernel");
         need(accumulate == 0 || accumulate == 1, "accumulate must be 0 or 1");
         if (!fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format not uploaded");
         need(fmt->v.M == 0 || O == 0 || dC, "null C");
         need(fmt->v.num_groups() == 0 || O == 0 || dB, "null B");
         need_device();
-        if (kernel == VCSR_KERNEL_AUTO) kernel = VCSR_KERNEL_ROW;
+        if (kernel == VCSR_KERNEL_AUTO) kernel = VCSR_KERNEL_TILE;
         hipStream_t st = (hipStream_t)stream;
         DeviceFmt& d = const_cast<vcsr_fmt*>(fmt)->dev;
-        if (kernel == VCSR_KERNEL_ROW && d.n_partials > 0 && d.partials_cols < O) {
+        const bool row_stationary = kernel == VCSR_KERNEL_ROW || kernel == VCSR_KERNEL_TILE;
+        if (row_stationary && d.partial_rows() > 0 && d.partials_cols < O) {
             // Scratch for the chunk sums of split rows, kept with the format.
             hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
             if (d.partials) hip_check(hipFree(d.partials), "hipFree");
             d.partials = nullptr;
             d.partials_cols = 0;
-            const size_t bytes = (size_t)d.n_partials * (size_t)O * sizeof(float);
+            const size_t bytes = (size_t)d.partial_rows() * (size_t)O * sizeof(float);
             hipError_t e = hipMalloc((void**)&d.partials, bytes);
             if (e == hipErrorOutOfMemory) throw vcsr::Error(VCSR_ENOMEM, "device allocation failed");
             hip_check(e, "hipMalloc partials");
@@ -314,6 +329,8 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
         run_timed(st, ms, [&]() -> hipError_t {
             if (kernel == VCSR_KERNEL_ROW)
                 return vcsr::launch_vcsr_rowmajor(fmt->v, d, dB, O, dC, accumulate, st);
+            if (kernel == VCSR_KERNEL_TILE)
+                return vcsr::launch_vcsr_tile(fmt->v, d, dB, O, dC, accumulate, st);
             if (!accumulate && bytesC > 0) {
                 hipError_t e = hipMemsetAsync(dC, 0, bytesC, st);
                 if (e != hipSuccess) return e;

@@ -1,0 +1,475 @@
+// vcsr_tile.hip - tile-stationary SpMM over the VCSR slots (gfx950).
+//
+// The arithmetic is the VCSR one: every nonzero is a packed slot s of the
+// format, contributing val[s] * B[seg_base + lcol[s], :] to its row.  The
+// schedule is the one that suits MI355X: a wavefront owns whole C rows and
+// writes them once with plain stores (no FP32 atomics, which cost about ten
+// plain stores each here), and rows that share columns are processed
+// together as a tile, so each B row slice is loaded once per tile and
+// applied to up to R rows held in registers.  On block-structured matrices
+// (FEM: the rows of a node's block row have the same columns) this divides
+// the B-row traffic through the vector memory pipe, the limiting resource of
+// a row-stationary SpMM, by the block height.
+//
+// Work item (one wave): MERGE consecutive work items of the view, each a run
+// of tile pieces with at most tile_chunk_entries(R) entries
+// (host/tile_view.hpp).
+// Phase 1 (lane per entry): read the entry's B row and R slot indices, gather
+// the R values from the VCSR value array and stage (B-row byte offset,
+// presence bits, values) in the wave's LDS list.
+// Phase 2, per column tile of LPE*VEC columns: the wave is S = 64/LPE
+// streams of LPE lanes; one load instruction serves one entry of every
+// stream.
+//  - Several pieces: each stream takes a contiguous run of whole pieces
+//    (balanced by entry count), accumulates the piece's R rows and stores
+//    them when its last entry has been applied.  No cross-lane reduction.
+//  - One piece (a long tile): the streams interleave over its entries and
+//    their sums are added with cross-lane shuffles before the store.
+// Loads are issued in blocks of U back to back before the block's FMAs; B is
+// read with raw buffer loads whose range check turns out-of-range offsets
+// into zeros, so inactive lanes and placeholder entries need no branch.
+// Rows absent from an entry are updated with a zero value (no per-row
+// select); this is exact for finite B.  A piece whose sum comes out
+// non-finite is recomputed with the presence bits before it is stored, so
+// inf / NaN in B reach exactly the rows the reference's loop reaches.
+#include <type_traits>
+
+#include "../host/tile_view.hpp"
+#include "common.hpp"
+#include "launch.hpp"
+#include "vecops.hpp"
+
+namespace vcsr {
+namespace {
+
+constexpr int kWaves = 4;
+// Buffer offset of "no B row": at least 2^31, above any buffer-path B size,
+// and still below 2^32 after adding a column offset (< 2^31).
+constexpr uint32_t kNoRow = 0x80000000u;
+
+template <int R>
+__device__ __forceinline__ void load_slots(const int32_t* __restrict__ p, int32_t (&s)[R]) {
+    if constexpr (R == 1) {
+        s[0] = p[0];
+    } else if constexpr (R == 2) {
+        const int2 x = *reinterpret_cast<const int2*>(p);
+        s[0] = x.x;
+        s[1] = x.y;
+    } else {
+#pragma unroll
+        for (int q = 0; q < R; q += 4) {
+            const int4 x = *reinterpret_cast<const int4*>(p + q);
+            s[q] = x.x;
+            s[q + 1] = x.y;
+            s[q + 2] = x.z;
+            s[q + 3] = x.w;
+        }
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void store_vals(float* p, const float (&a)[R]) {
+    if constexpr (R == 1) {
+        p[0] = a[0];
+    } else if constexpr (R == 2) {
+        *reinterpret_cast<float2*>(p) = make_float2(a[0], a[1]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < R; q += 4)
+            *reinterpret_cast<float4*>(p + q) = make_float4(a[q], a[q + 1], a[q + 2], a[q + 3]);
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void load_vals(const float* p, float (&a)[R]) {
+    if constexpr (R == 1) {
+        a[0] = p[0];
+    } else if constexpr (R == 2) {
+        const float2 x = *reinterpret_cast<const float2*>(p);
+        a[0] = x.x;
+        a[1] = x.y;
+    } else {
+#pragma unroll
+        for (int q = 0; q < R; q += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(p + q);
+            a[q] = x.x;
+            a[q + 1] = x.y;
+            a[q + 2] = x.z;
+            a[q + 3] = x.w;
+        }
+    }
+}
+
+__device__ __forceinline__ bool all_finite(float x) { return __builtin_isfinite(x); }
+__device__ __forceinline__ bool all_finite(float2 x) {
+    return __builtin_isfinite(x.x) && __builtin_isfinite(x.y);
+}
+__device__ __forceinline__ bool all_finite(float4 x) {
+    return __builtin_isfinite(x.x) && __builtin_isfinite(x.y) && __builtin_isfinite(x.z) &&
+           __builtin_isfinite(x.w);
+}
+
+// One wave per MERGE consecutive work items of the view.  BUF: B smaller than
+// 2 GB, read with raw buffer loads at 32-bit byte offsets; otherwise 64-bit
+// addresses from B row indices (LPE = 64 only).
+template <int VEC, int LPE, int R, int MERGE, bool BUF>
+__global__ __launch_bounds__(256) void vcsr_tile_kernel(
+    int32_t n_chunks, int32_t O, int32_t accumulate, uint32_t b_bytes,
+    const int4* __restrict__ chunks, const int4* __restrict__ pieces,
+    const int32_t* __restrict__ ent_brow, const int32_t* __restrict__ ent_slot,
+    const float* __restrict__ val, const float* __restrict__ B, float* __restrict__ C,
+    float* __restrict__ partials) {
+    using V = typename VecT<VEC>::T;
+    constexpr int S = 64 / LPE;                              // streams per wave
+    constexpr int EMAX = tile_chunk_entries(R) * MERGE;      // entries per wave
+    constexpr int PMAX = kTileChunkPieces * MERGE;           // pieces per wave
+    constexpr int U = 8;                                     // loads per block
+    __shared__ uint32_t s_brow[kWaves][EMAX];
+    __shared__ uint8_t s_mask[kWaves][EMAX];
+    __shared__ uint8_t s_bad[kWaves][PMAX];
+    __shared__ __align__(16) float s_val[kWaves][EMAX * R];
+    __shared__ int4 s_piece[kWaves][PMAX + 2];
+    __shared__ int32_t s_first[kWaves][S + 1];
+
+    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+    const int32_t w = (int32_t)(xcd_remap(blockIdx.x, gridDim.x) * kWaves) + wave;
+    const int32_t c0 = w * MERGE;
+    if (c0 >= n_chunks) return;
+    const int32_t c1 = min(n_chunks, c0 + MERGE) - 1;
+    uint32_t* lb = s_brow[wave];
+    uint8_t* lm = s_mask[wave];
+    uint8_t* lbad = s_bad[wave];
+    float* lv = s_val[wave];
+    int4* lp = s_piece[wave];
+    int32_t* lf = s_first[wave];
+    const int32_t e0 = uniform(chunks[c0].x), ne = uniform(chunks[c1].y) - e0;  // <= EMAX
+    const int32_t p0 = uniform(chunks[c0].z), np = uniform(chunks[c1].w) - p0;  // <= PMAX
+
+    // Phase 1: stage the entries and the piece table.
+    const uint32_t row_bytes = (uint32_t)O * 4u;
+    for (int32_t i = lane; i < ne; i += 64) {
+        const int64_t e = (int64_t)e0 + i;
+        int32_t sl[R];
+        load_slots<R>(ent_slot + e * R, sl);
+        const uint32_t br = (uint32_t)ent_brow[e];
+        float a[R];
+        uint32_t m = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            a[r] = 0.f;
+            if (sl[r] >= 0) {
+                a[r] = val[sl[r]];
+                m |= 1u << r;
+            }
+        }
+        lb[i] = BUF ? (m ? br * row_bytes : kNoRow) : br;
+        lm[i] = (uint8_t)m;
+        store_vals<R>(lv + i * R, a);
+    }
+    for (int32_t j = lane; j < np; j += 64) {
+        int4 pc = pieces[p0 + j];
+        pc.z -= e0;
+        lp[j] = pc;
+        lbad[j] = 0;
+    }
+    if (lane < 2) lp[np + lane] = make_int4(0, 0, ne, -1);  // end sentinels
+    wave_sync();
+
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), (short)0, (int)b_bytes,
+                                          kRawBufferFlags);
+    const int sub = lane / LPE, kl = lane % LPE;
+
+    // One entry's B slice; zeros for "no row" (placeholders, lanes past the
+    // end) on the buffer path.
+    auto load_b = [&](int32_t tc, bool ok, uint32_t koff) -> V {
+        if constexpr (BUF) {
+            const uint32_t off = ok ? lb[tc] + koff : kNoRow;
+            return load_b_buf<VEC>(rsrc, off);
+        } else {
+            const V b = *reinterpret_cast<const V*>(B + (int64_t)lb[tc] * O + koff / 4);
+            return ok ? b : zero_vec(V());
+        }
+    };
+    // acc[r] += a[r] * b for every tile row; absent rows have a[r] = 0, which
+    // is exact while b is finite.  A non-finite b reaching an absent row
+    // (0 * inf = NaN) shows up as a non-finite row sum at the store, and the
+    // piece is then recomputed with the presence bits (redo_piece).
+    auto apply = [&](V (&acc)[R], int32_t tc, bool ok, const V& b) {
+        float a[R];
+        load_vals<R>(lv + tc * R, a);
+#pragma unroll
+        for (int r = 0; r < R; ++r) fma_vec(acc[r], ok ? a[r] : 0.f, b);
+    };
+    // Whether every value this lane would write for piece pidx is finite.
+    auto piece_finite = [&](int32_t pidx, const V (&acc)[R], bool kok) -> bool {
+        const int32_t rows = lp[pidx].y;
+        bool fin = true;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (r < rows) fin = fin && all_finite(acc[r]);
+        return fin || !kok;
+    };
+    // Writes the accumulated rows of piece pidx (its first pc.y rows exist)
+    // to C or to its partial rows.
+    auto store_piece = [&](int32_t pidx, const V (&acc)[R], int32_t k, bool kok) {
+        const int4 pc = lp[pidx];
+        if (!kok) return;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r >= pc.y) break;
+            if (pc.w < 0) {
+                V* dst = reinterpret_cast<V*>(C + (int64_t)(pc.x + r) * O + k);
+                *dst = accumulate ? add_vec(*dst, acc[r]) : acc[r];
+            } else {
+                *reinterpret_cast<V*>(partials + (int64_t)(pc.w + r) * O + k) = acc[r];
+            }
+        }
+    };
+    // Exact recomputation of piece q in entry order, skipping absent rows
+    // (taken only for pieces whose sum is not finite, which were not stored).
+    auto redo_piece = [&](int32_t q, int32_t k, uint32_t koff, bool kok) {
+        V acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
+        for (int32_t t = lp[q].z; t < lp[q + 1].z; ++t) {
+            const V b = load_b(t, true, koff);
+            float a[R];
+            load_vals<R>(lv + t * R, a);
+            const uint32_t m = lm[t];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if ((m >> r) & 1u) fma_vec(acc[r], a[r], b);
+        }
+        store_piece(q, acc, k, kok);
+    };
+
+    if (np > 1) {
+        // Stream s takes the pieces whose entry midpoint falls in the s-th
+        // S-quantile of the item: first piece lf[s], end piece lf[s + 1].
+        if (lane <= S) {
+            int32_t lo = 0, hi = np;
+            while (lo < hi) {
+                const int32_t mid = (lo + hi) >> 1;
+                const int32_t sm = ((lp[mid].z + lp[mid + 1].z) * S) / (2 * ne);
+                if (sm < lane) lo = mid + 1;
+                else hi = mid;
+            }
+            lf[lane] = lo;
+        }
+        wave_sync();
+        const int32_t pa = lf[sub], pb = lf[sub + 1];
+        const int32_t tb = lp[pa].z, te = lp[pb].z;  // this stream's entries
+        // Lanes of this lane's stream, for ballots.
+        const uint64_t smask =
+            LPE == 64 ? ~0ull : (((1ull << (LPE & 63)) - 1ull) << ((sub * LPE) & 63));
+        int32_t nmax = te - tb, nmin = te - tb;
+#pragma unroll
+        for (int sh = LPE; sh < 64; sh <<= 1) {
+            nmax = max(nmax, __shfl_xor(nmax, sh));
+            nmin = min(nmin, __shfl_xor(nmin, sh));
+        }
+        nmax = uniform(nmax);
+        nmin = uniform(nmin);
+        for (int32_t k0 = 0; k0 < O; k0 += LPE * VEC) {
+            const int32_t k = k0 + kl * VEC;
+            const bool kok = k < O;
+            const uint32_t koff = (uint32_t)((kok || BUF) ? k : 0) * 4u;
+            V acc[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
+            int32_t p = pa, pend = lp[pa + 1].z;
+            bool bad = false;
+            auto block = [&](auto full_c, int32_t i0) {
+                constexpr bool FULL = decltype(full_c)::value;
+                V b[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int32_t t = tb + i0 + u;
+                    const bool ok = FULL || t < te;
+                    b[u] = load_b(ok ? t : 0, ok, koff);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int32_t t = tb + i0 + u;
+                    const bool ok = FULL || t < te;
+                    apply(acc, ok ? t : 0, ok, b[u]);
+                    if (ok && t + 1 == pend) {
+                        // A stream stores a piece only if all its lanes' sums
+                        // are finite; otherwise redo_piece computes and stores
+                        // it after the loop.
+                        const uint64_t bm = __ballot(!piece_finite(p, acc, kok));
+                        if ((bm & smask) != 0) {
+                            bad = true;
+                            lbad[p] = 1;
+                        } else {
+                            store_piece(p, acc, k, kok);
+                        }
+#pragma unroll
+                        for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
+                        ++p;
+                        pend = lp[p + 1].z;
+                    }
+                }
+            };
+            for (int32_t i0 = 0; i0 < nmax; i0 += U) {
+                if (i0 + U <= nmin) block(std::true_type(), i0);
+                else block(std::false_type(), i0);
+            }
+            if (__any(bad)) {
+                wave_sync();
+                for (int32_t q = pa; q < pb; ++q)
+                    if (lbad[q]) redo_piece(q, k, koff, kok);
+                wave_sync();
+                for (int32_t q = pa; q < pb; ++q) lbad[q] = 0;
+                wave_sync();
+            }
+        }
+    } else {
+        // One piece: entries t = sub + S*i, summed across streams at the end.
+        const int32_t nper = (ne + S - 1) / S, nfull = ne / S;
+        for (int32_t k0 = 0; k0 < O; k0 += LPE * VEC) {
+            const int32_t k = k0 + kl * VEC;
+            const bool kok = k < O;
+            const uint32_t koff = (uint32_t)((kok || BUF) ? k : 0) * 4u;
+            V acc[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
+            auto block = [&](auto full_c, int32_t i0) {
+                constexpr bool FULL = decltype(full_c)::value;
+                V b[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int32_t t = sub + S * (i0 + u);
+                    const bool ok = FULL || t < ne;
+                    b[u] = load_b(ok ? t : 0, ok, koff);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int32_t t = sub + S * (i0 + u);
+                    const bool ok = FULL || t < ne;
+                    apply(acc, ok ? t : 0, ok, b[u]);
+                }
+            };
+            for (int32_t i0 = 0; i0 < nper; i0 += U) {
+                if (i0 + U <= nfull) block(std::true_type(), i0);
+                else block(std::false_type(), i0);
+            }
+#pragma unroll
+            for (int sh = LPE; sh < 64; sh <<= 1) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] = add_vec(acc[r], shfl_xor_vec(acc[r], sh));
+            }
+            // Stream 0 stores the sum, or recomputes it exactly when any of
+            // its lanes' values is not finite.
+            const bool bad = sub == 0 && !piece_finite(0, acc, kok);
+            if (__any(bad)) {
+                if (sub == 0) redo_piece(0, k, koff, kok);
+            } else if (sub == 0) {
+                store_piece(0, acc, k, kok);
+            }
+        }
+    }
+}
+
+// Adds the piece partials of every row of a split tile into C (one wave per
+// row and 64*VEC-column tile).  split: {row, first partial row, stride, pieces}.
+template <int VEC>
+__global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t n_units, int32_t nkt, int32_t O,
+                                                        int32_t accumulate,
+                                                        const int4* __restrict__ split,
+                                                        const float* __restrict__ partials,
+                                                        float* __restrict__ C) {
+    using V = typename VecT<VEC>::T;
+    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+    const int32_t unit = (int32_t)(blockIdx.x * kWaves) + wave;
+    if (unit >= n_units) return;
+    const int32_t item = unit / nkt, kt = unit - item * nkt;
+    const int4 s = split[item];
+    const int32_t k = kt * 64 * VEC + lane * VEC;
+    if (k >= O) return;
+    V acc = zero_vec(V());
+    for (int32_t j = 0; j < s.w; ++j)
+        acc = add_vec(acc, *reinterpret_cast<const V*>(
+                               partials + (int64_t)(s.y + (int64_t)j * s.z) * O + k));
+    V* dst = reinterpret_cast<V*>(C + (int64_t)s.x * O + k);
+    *dst = accumulate ? add_vec(*dst, acc) : acc;
+}
+
+template <int VEC, int LPE, int R, bool BUF>
+hipError_t launch_one(const DeviceFmt& d, const float* B, int32_t O, float* C,
+                      int32_t accumulate, uint32_t b_bytes, hipStream_t st) {
+    // Eight or more streams per wave (B slices of at most 32 columns): four
+    // work items per wave, so each stream still gets several tiles.
+    constexpr int MERGE = (64 / LPE >= 8 && R < 8) ? 4 : 1;
+    const int64_t waves = ((int64_t)d.tv_n_chunks + MERGE - 1) / MERGE;
+    const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves)), block(64 * kWaves);
+    hipLaunchKernelGGL((vcsr_tile_kernel<VEC, LPE, R, MERGE, BUF>), grid, block, 0, st, d.tv_n_chunks, O,
+                       accumulate, b_bytes, reinterpret_cast<const int4*>(d.tv_chunks),
+                       reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_slot, d.val, B,
+                       C, d.partials);
+    return hipGetLastError();
+}
+
+template <int VEC, int R>
+hipError_t launch_r(const DeviceFmt& d, const float* B, int32_t O, float* C, int32_t accumulate,
+                    uint64_t b_bytes, hipStream_t st) {
+    if (b_bytes + 64u * 4u * (uint64_t)VEC >= kBufferLimit)
+        return launch_one<VEC, 64, R, false>(d, B, O, C, accumulate, 0u, st);
+    const uint32_t bb = (uint32_t)b_bytes;
+    // Lanes per entry: the smallest power of two covering O, at least 8 (at
+    // most 8 streams per wave, so every stream gets several tiles).  VEC
+    // below 4 is chosen only when O is too narrow for 16 lanes of 4 floats
+    // (or B/C are not 16-byte aligned); then LPE = 8 occurs for VEC = 1 only.
+    const int32_t need = (O + VEC - 1) / VEC;
+    if constexpr (VEC == 1) {
+        if (need <= 8) return launch_one<VEC, 8, R, true>(d, B, O, C, accumulate, bb, st);
+    }
+    if (need <= 16) return launch_one<VEC, 16, R, true>(d, B, O, C, accumulate, bb, st);
+    if (need <= 32) return launch_one<VEC, 32, R, true>(d, B, O, C, accumulate, bb, st);
+    return launch_one<VEC, 64, R, true>(d, B, O, C, accumulate, bb, st);
+}
+
+template <int VEC>
+hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, float* C,
+                      int32_t accumulate, hipStream_t st) {
+    if (d.tv_n_chunks > 0) {
+        const uint64_t b_bytes = (uint64_t)v.N * (uint64_t)O * 4u;
+        hipError_t e;
+        switch (d.tv_R) {
+            case 1: e = launch_r<VEC, 1>(d, B, O, C, accumulate, b_bytes, st); break;
+            case 2: e = launch_r<VEC, 2>(d, B, O, C, accumulate, b_bytes, st); break;
+            case 4: e = launch_r<VEC, 4>(d, B, O, C, accumulate, b_bytes, st); break;
+            case 8: e = launch_r<VEC, 8>(d, B, O, C, accumulate, b_bytes, st); break;
+            default: return hipErrorInvalidValue;
+        }
+        if (e != hipSuccess) return e;
+    }
+    if (d.tv_n_split > 0) {
+        const int32_t nkt = (O + 64 * VEC - 1) / (64 * VEC);
+        const int64_t ru = (int64_t)d.tv_n_split * nkt;
+        if (ru > INT32_MAX) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(vcsr_tile_reduce<VEC>, dim3((unsigned)((ru + kWaves - 1) / kWaves)),
+                           dim3(64 * kWaves), 0, st, (int32_t)ru, nkt, O, accumulate,
+                           reinterpret_cast<const int4*>(d.tv_split), d.partials, C);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                            float* C, int32_t accumulate, hipStream_t st) {
+    if (O <= 0 || v.M == 0) return hipSuccess;
+    const bool a16 = (((uintptr_t)B | (uintptr_t)C) & 15u) == 0;
+    const bool a8 = (((uintptr_t)B | (uintptr_t)C) & 7u) == 0;
+    // The vector memory pipe moves about 64 bytes per clock whatever the
+    // load width, so narrow rows lose nothing with narrower per-lane vectors
+    // and gain streams of at least 16 lanes (fewer streams per wave).
+    if (O % 4 == 0 && a16 && O >= 64) return launch_vec<4>(v, d, B, O, C, accumulate, st);
+    if (O % 2 == 0 && a8 && O >= 32) return launch_vec<2>(v, d, B, O, C, accumulate, st);
+    return launch_vec<1>(v, d, B, O, C, accumulate, st);
+}
+
+}  // namespace vcsr

@@ -36,8 +36,22 @@ struct DeviceFmt {
     int32_t n_partials = 0;             // chunks of split rows
     int32_t* split_rows = nullptr;      // 3*n_split: {row, first partial, partial count}
     int32_t n_split = 0;
-    float* partials = nullptr;          // n_partials * partials_cols floats, grown on demand
+    // Row-tile view (host/tile_view.hpp) walked by the tile-stationary kernel.
+    int32_t tv_R = 1;                   // accumulator rows per tile
+    int32_t* tv_chunks = nullptr;       // 4*tv_n_chunks: entry range, piece range
+    int32_t tv_n_chunks = 0;
+    int32_t* tv_pieces = nullptr;       // 4 per piece: row, rows, first entry, partial row
+    int32_t* tv_brow = nullptr;         // per entry: B row
+    int32_t* tv_slot = nullptr;         // tv_R per entry: VCSR slot or -1
+    int64_t tv_n_entries = 0;
+    int32_t* tv_split = nullptr;        // 4*tv_n_split: row, partial row, stride, pieces
+    int32_t tv_n_split = 0;
+    int32_t tv_partial_rows = 0;
+    // Partial sums of split rows / tiles: partial_rows() rows of
+    // partials_cols floats, grown on demand.
+    float* partials = nullptr;
     int64_t partials_cols = 0;
+    int32_t partial_rows() const { return n_partials > tv_partial_rows ? n_partials : tv_partial_rows; }
 };
 
 struct vcsr_coo {
@@ -49,6 +63,8 @@ struct vcsr_csr {
 struct vcsr_fmt {
     vcsr::Vcsr v;
     DeviceFmt dev;
+    int32_t tile_rows = 0;  // requested tile height of the row-tile view (0 = automatic)
+    int64_t tv_tiles = 0;   // tiles of the uploaded view
 };
 
 namespace vcsr {

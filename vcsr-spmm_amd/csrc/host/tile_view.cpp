@@ -1,0 +1,271 @@
+// tile_view.cpp - builds the row-tile view of a VCSR format (tile_view.hpp).
+//
+// Everything is recovered from the packed VCSR arrays (group_ptr,
+// group_depth, group_seg_base, group_rows, lcol); the view holds indices
+// into them, never copies of the values.
+#include "tile_view.hpp"
+
+#include <algorithm>
+#include <numeric>
+#include <string>
+
+#include "parallel.hpp"
+
+namespace vcsr {
+namespace {
+
+constexpr int kErange = 5;  // VCSR_ERANGE
+constexpr int kEinval = 1;  // VCSR_EINVAL
+
+// Entries of every row as (column, slot), row r at [ptr[r], ptr[r+1]), in
+// column order.
+struct RowLists {
+    std::vector<int64_t> ptr;
+    std::vector<int32_t> col, slot;
+};
+
+int32_t lane_entries(const Vcsr& v, int32_t g, int32_t l) {
+    const int64_t s0 = (int64_t)v.group_ptr[g] + l;
+    int32_t c = 0;
+    while (c < v.group_depth[g] && v.lcol[(size_t)(s0 + (int64_t)c * v.bundle)] >= 0) ++c;
+    return c;
+}
+
+RowLists row_lists(const Vcsr& v, int nthreads) {
+    const int32_t G = v.num_groups(), M = v.M, b = v.bundle;
+    RowLists rl;
+    rl.ptr.assign((size_t)M + 1, 0);
+    for (int32_t g = 0; g < G; ++g) {
+        for (int32_t l = 0; l < b; ++l) {
+            const int32_t c = lane_entries(v, g, l);
+            if (c == 0) continue;
+            const int32_t row = v.group_rows[(size_t)g * b + l];
+            if (row < 0 || row >= M) throw Error(kEinval, "group row out of range");
+            rl.ptr[(size_t)row + 1] += c;
+        }
+    }
+    for (int32_t r = 0; r < M; ++r) rl.ptr[(size_t)r + 1] += rl.ptr[(size_t)r];
+    const int64_t total = rl.ptr[(size_t)M];
+    rl.col.resize((size_t)total);
+    rl.slot.resize((size_t)total);
+    std::vector<int64_t> cur(rl.ptr.begin(), rl.ptr.end() - 1);
+    for (int32_t g = 0; g < G; ++g) {
+        const int32_t base = v.group_seg_base[g];
+        for (int32_t l = 0; l < b; ++l) {
+            const int32_t c = lane_entries(v, g, l);
+            if (c == 0) continue;
+            int64_t& at = cur[(size_t)v.group_rows[(size_t)g * b + l]];
+            for (int32_t d = 0; d < c; ++d) {
+                const int64_t s = (int64_t)v.group_ptr[g] + l + (int64_t)d * b;
+                rl.col[(size_t)at] = base + v.lcol[(size_t)s];
+                rl.slot[(size_t)at] = (int32_t)s;
+                ++at;
+            }
+        }
+    }
+    // Groups come in segment order and a lane's slots in local-column order,
+    // so rows are already sorted; sort any row that is not (stable, so equal
+    // columns keep their slot order).
+    parallel_for(M, 4096, nthreads, [&](int64_t rb, int64_t re) {
+        std::vector<std::pair<int32_t, int32_t>> tmp;
+        for (int64_t r = rb; r < re; ++r) {
+            const int64_t a = rl.ptr[(size_t)r], e = rl.ptr[(size_t)r + 1];
+            if (std::is_sorted(rl.col.begin() + a, rl.col.begin() + e)) continue;
+            tmp.clear();
+            for (int64_t i = a; i < e; ++i) tmp.emplace_back(rl.col[(size_t)i], rl.slot[(size_t)i]);
+            std::stable_sort(tmp.begin(), tmp.end(),
+                             [](const auto& x, const auto& y) { return x.first < y.first; });
+            for (int64_t i = a; i < e; ++i) {
+                rl.col[(size_t)i] = tmp[(size_t)(i - a)].first;
+                rl.slot[(size_t)i] = tmp[(size_t)(i - a)].second;
+            }
+        }
+    });
+    return rl;
+}
+
+// Sorted multiset union: every column kept with the larger of its two
+// multiplicities.
+void union_into(const std::vector<int32_t>& a, const int32_t* b, size_t nb,
+                std::vector<int32_t>& out) {
+    out.clear();
+    size_t i = 0, j = 0;
+    while (i < a.size() && j < nb) {
+        if (a[i] < b[j]) {
+            out.push_back(a[i++]);
+        } else if (b[j] < a[i]) {
+            out.push_back(b[j++]);
+        } else {
+            out.push_back(a[i]);
+            ++i;
+            ++j;
+        }
+    }
+    out.insert(out.end(), a.begin() + (int64_t)i, a.end());
+    out.insert(out.end(), b + j, b + nb);
+}
+
+struct Tile {
+    int32_t row0, nrows;
+    int64_t nent;  // union size; 1 for a tile of empty rows (one placeholder entry)
+};
+
+// Greedy tiles of at most `cap` consecutive rows inside [r0, r1): the next
+// row joins the tile while at least half of its columns are already in the
+// tile's union (empty rows always join).
+void tile_rows(const RowLists& rl, int32_t r0, int32_t r1, int32_t cap, std::vector<Tile>& out) {
+    std::vector<int32_t> u, w;
+    int32_t i = r0;
+    while (i < r1) {
+        u.assign(rl.col.begin() + rl.ptr[(size_t)i], rl.col.begin() + rl.ptr[(size_t)i + 1]);
+        int32_t n = 1;
+        while (n < cap && i + n < r1) {
+            const int32_t r = i + n;
+            const size_t len = (size_t)(rl.ptr[(size_t)r + 1] - rl.ptr[(size_t)r]);
+            union_into(u, rl.col.data() + rl.ptr[(size_t)r], len, w);
+            if ((w.size() - u.size()) * 2 > len) break;
+            u.swap(w);
+            ++n;
+        }
+        out.push_back({i, n, std::max<int64_t>(1, (int64_t)u.size())});
+        i += n;
+    }
+}
+
+std::vector<Tile> make_tiles(const RowLists& rl, int32_t M, int32_t cap, int nthreads) {
+    const int32_t nblk = (M + kTileRowBlock - 1) / kTileRowBlock;
+    std::vector<std::vector<Tile>> per((size_t)nblk);
+    parallel_for(nblk, 1, nthreads, [&](int64_t bb, int64_t be) {
+        for (int64_t blk = bb; blk < be; ++blk) {
+            const int32_t r0 = (int32_t)blk * kTileRowBlock;
+            tile_rows(rl, r0, std::min(M, r0 + kTileRowBlock), cap, per[(size_t)blk]);
+        }
+    });
+    std::vector<Tile> tiles;
+    for (auto& p : per) tiles.insert(tiles.end(), p.begin(), p.end());
+    return tiles;
+}
+
+}  // namespace
+
+TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
+    if (R != 0 && R != 1 && R != 2 && R != 4 && R != 8)
+        throw Error(kEinval, "tile height must be 0, 1, 2, 4 or 8");
+    if (nthreads <= 0) nthreads = default_threads();
+    const int32_t M = v.M;
+    const RowLists rl = row_lists(v, nthreads);
+
+    // Tile height: modelled cost per union entry = one B-row slice load
+    // (about 16 cycles of the vector memory pipe) + R accumulator updates.
+    std::vector<Tile> tiles;
+    if (R == 0) {
+        double best = 0;
+        for (int32_t cap : {1, 2, 4, 8}) {
+            std::vector<Tile> t = make_tiles(rl, M, cap, nthreads);
+            int64_t ent = 0;
+            for (const Tile& x : t) ent += x.nent;
+            const double cost = (double)ent * (16.0 + cap);
+            if (R == 0 || cost < best) {
+                best = cost;
+                R = cap;
+                tiles.swap(t);
+            }
+            // No sharing between neighbouring rows: taller tiles only cost.
+            if (cap == 2 && R == 1) break;
+        }
+    } else {
+        tiles = make_tiles(rl, M, R, nthreads);
+    }
+
+    TileView tv;
+    tv.R = R;
+    tv.n_tiles = (int32_t)tiles.size();
+    std::vector<int64_t> eoff(tiles.size() + 1, 0);
+    for (size_t t = 0; t < tiles.size(); ++t) eoff[t + 1] = eoff[t] + tiles[t].nent;
+    const int64_t E = eoff.back();
+    if (E > INT32_MAX) throw Error(kErange, "tile view has too many entries");
+    tv.brow.resize((size_t)E);
+    tv.slot.assign((size_t)E * (size_t)R, -1);
+    parallel_for((int64_t)tiles.size(), 1024, nthreads, [&](int64_t tb, int64_t te) {
+        std::vector<int32_t> u, w;
+        for (int64_t t = tb; t < te; ++t) {
+            const Tile& x = tiles[(size_t)t];
+            u.clear();
+            for (int32_t r = 0; r < x.nrows; ++r) {
+                const int64_t a = rl.ptr[(size_t)(x.row0 + r)], e = rl.ptr[(size_t)(x.row0 + r) + 1];
+                union_into(u, rl.col.data() + a, (size_t)(e - a), w);
+                u.swap(w);
+            }
+            const int64_t e0 = eoff[(size_t)t];
+            if (u.empty()) {
+                tv.brow[(size_t)e0] = 0;  // placeholder entry: every slot -1
+                continue;
+            }
+            for (size_t q = 0; q < u.size(); ++q) tv.brow[(size_t)e0 + q] = u[q];
+            for (int32_t r = 0; r < x.nrows; ++r) {
+                int64_t p = rl.ptr[(size_t)(x.row0 + r)];
+                const int64_t pe = rl.ptr[(size_t)(x.row0 + r) + 1];
+                for (size_t q = 0; q < u.size() && p < pe; ++q) {
+                    if (rl.col[(size_t)p] == u[q]) {
+                        tv.slot[((size_t)e0 + q) * (size_t)R + (size_t)r] = rl.slot[(size_t)p];
+                        ++p;
+                    }
+                }
+            }
+        }
+    });
+
+    // Work items.  A tile longer than half a work item's entry budget gets
+    // work items of its own (cut into equal pieces that write partial sums
+    // when it exceeds the budget); shorter tiles are packed in row order.
+    const int32_t cap_e = tile_chunk_entries(R);
+    int64_t ce0 = 0, cent = 0;
+    int32_t cp0 = 0;
+    auto close_chunk = [&](int64_t next_e) {
+        const int32_t np = (int32_t)(tv.pieces.size() / 4);
+        if (np > cp0)
+            tv.chunks.insert(tv.chunks.end(), {(int32_t)ce0, (int32_t)(ce0 + cent), cp0, np});
+        ce0 = next_e;
+        cent = 0;
+        cp0 = np;
+    };
+    int64_t n_partial = 0;
+    for (size_t t = 0; t < tiles.size(); ++t) {
+        const Tile& x = tiles[t];
+        const int64_t e0 = eoff[t];
+        if (x.nent > cap_e / 2) {
+            close_chunk(e0);
+            const int64_t npc = (x.nent + cap_e - 1) / cap_e;
+            const int64_t size = (x.nent + npc - 1) / npc;
+            const int64_t base = n_partial;
+            for (int64_t j = 0; j < npc; ++j) {
+                const int64_t a = e0 + j * size, e = std::min(e0 + x.nent, a + size);
+                const int32_t pi = (int32_t)(tv.pieces.size() / 4);
+                tv.pieces.insert(tv.pieces.end(),
+                                 {x.row0, x.nrows, (int32_t)a,
+                                  npc == 1 ? -1 : (int32_t)(base + j * x.nrows)});
+                tv.chunks.insert(tv.chunks.end(), {(int32_t)a, (int32_t)e, pi, pi + 1});
+            }
+            if (npc > 1) {
+                for (int32_t r = 0; r < x.nrows; ++r)
+                    tv.split.insert(tv.split.end(),
+                                    {x.row0 + r, (int32_t)(base + r), x.nrows, (int32_t)npc});
+                n_partial += npc * x.nrows;
+                if (n_partial > INT32_MAX) throw Error(kErange, "too many partial rows");
+            }
+            cp0 = (int32_t)(tv.pieces.size() / 4);
+            ce0 = e0 + x.nent;
+            cent = 0;
+            continue;
+        }
+        if (cent + x.nent > cap_e || (int32_t)(tv.pieces.size() / 4) - cp0 == kTileChunkPieces)
+            close_chunk(e0);
+        tv.pieces.insert(tv.pieces.end(), {x.row0, x.nrows, (int32_t)e0, -1});
+        cent += x.nent;
+    }
+    close_chunk(E);
+    tv.n_partial_rows = (int32_t)n_partial;
+    return tv;
+}
+
+}  // namespace vcsr

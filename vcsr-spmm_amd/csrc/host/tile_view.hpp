@@ -1,0 +1,52 @@
+// tile_view.hpp - the row-tile view of a VCSR format that the
+// tile-stationary kernel (device/vcsr_tile.hip) walks.
+//
+// A tile is a run of at most R consecutive rows that share most of their
+// columns (the rows of one block row of a block-structured matrix).  Its
+// entries are the union of the rows' columns in column order; entry e holds
+// the B row it reads and, for every row r of the tile, the VCSR slot whose
+// value multiplies that B row for row r (-1 where row r has no such column).
+// Each B row slice is then loaded once per tile instead of once per row.
+// The values stay in the VCSR slot array; the view only indexes them.
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+#include "core.hpp"
+
+namespace vcsr {
+
+// Entries of one work item, by tile height R.  Small items keep many waves in
+// flight when each entry is a long B-row slice; for narrow B the kernel
+// merges several consecutive items per wave.
+constexpr int32_t tile_chunk_entries(int32_t R) { return R >= 8 ? 256 : 128; }
+// Tile pieces per work item.
+constexpr int32_t kTileChunkPieces = 32;
+// Rows are cut into tiles inside fixed blocks of this many rows (so that
+// blocks can be tiled in parallel and the view never depends on the thread
+// count).
+constexpr int32_t kTileRowBlock = 4096;
+
+struct TileView {
+    int32_t R = 1;                // accumulator rows per tile: 1, 2, 4 or 8
+    int32_t n_tiles = 0;
+    // Work items, 4 ints each: first entry, end entry, first piece, end piece.
+    std::vector<int32_t> chunks;
+    // Tile pieces, 4 ints each: first row, row count, first entry, and the
+    // first partial row (pieces of a split tile) or -1 (the piece writes C).
+    std::vector<int32_t> pieces;
+    std::vector<int32_t> brow;    // per entry: B row = segment base + local column
+    std::vector<int32_t> slot;    // R per entry: VCSR slot for tile row r, or -1
+    // Rows of split tiles, 4 ints each: row, first partial row, stride
+    // between the piece partials of that row, piece count.
+    std::vector<int32_t> split;
+    int32_t n_partial_rows = 0;
+    int64_t n_entries() const { return (int64_t)brow.size(); }
+};
+
+// Builds the view.  R = 0 picks the tile height that minimises the modelled
+// cost (B-row loads plus accumulator updates); R = 1, 2, 4 or 8 forces it.
+TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads);
+
+}  // namespace vcsr
