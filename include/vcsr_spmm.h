@@ -137,7 +137,7 @@ int vcsr_fmt_arrays(const vcsr_fmt* fmt, vcsr_arrays* out);
  * src/vcsr_seg.cu:196-211.  The handle owns the device copy: no globals. */
 int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream);
 /* Tile height of the row-tile view vcsr_fmt_upload derives for the
- * tile-stationary kernel (VCSR_KERNEL_TILE): rows = 1, 2, 4 or 8 forces it,
+ * tile-stationary kernel (VCSR_KERNEL_TILE): rows = 1, 2, 3, 4 or 8 forces it,
  * 0 (the default) picks it from the matrix.  Only before the upload
  * (VCSR_ESTATE after).  No reference counterpart. */
 int vcsr_fmt_set_tile_rows(vcsr_fmt* fmt, int32_t rows);

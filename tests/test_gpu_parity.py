@@ -300,7 +300,7 @@ def _block_csr(vs, rng, nbr, bh, N, blocks_per_row, bw, keep):
 
 
 @pytest.mark.parametrize("bh,tile_rows", [(2, 0), (3, 0), (4, 0), (8, 0), (16, 0), (3, 1), (3, 2),
-                                          (3, 8), (5, 4)])
+                                          (3, 3), (6, 3), (3, 8), (5, 4)])
 @pytest.mark.parametrize("O", [1, 8, 33, 128, 200, 520])
 def test_tile_kernel_block_rows(gpu, orc, st, bh, tile_rows, O):
     vs = gpu
@@ -325,7 +325,7 @@ def test_tile_kernel_block_rows(gpu, orc, st, bh, tile_rows, O):
         assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"bh{bh} R{R} O{O}")
 
 
-@pytest.mark.parametrize("tile_rows", [1, 4, 8])
+@pytest.mark.parametrize("tile_rows", [1, 3, 4, 8])
 def test_tile_kernel_split_tiles(gpu, orc, st, tile_rows):
     """Block rows wider than one work item: tiles are cut into pieces whose
     partial sums a second kernel adds; wider O grows the scratch."""

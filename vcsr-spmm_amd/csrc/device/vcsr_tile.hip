@@ -111,9 +111,13 @@ __device__ __forceinline__ bool all_finite(float4 x) {
 
 // One wave per MERGE consecutive work items of the view.  BUF: B smaller than
 // 2 GB, read with raw buffer loads at 32-bit byte offsets; otherwise 64-bit
-// addresses from B row indices (LPE = 64 only).
+// addresses from B row indices (LPE = 64 only).  Up to 3 tile rows (one work
+// item per wave) the register budget is held to 5 waves per SIMD: measured
+// faster than 4 on the banded workload; 6 spills, and so does 5 with 4 rows.
 template <int VEC, int LPE, int R, int MERGE, bool BUF>
-__global__ __launch_bounds__(256) void vcsr_tile_kernel(
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu((R <= 3 && MERGE == 1) ? 5 : 1, 8)))
+void vcsr_tile_kernel(
     int32_t n_chunks, int32_t O, int32_t accumulate, uint32_t b_bytes,
     const int4* __restrict__ chunks, const int4* __restrict__ pieces,
     const int32_t* __restrict__ ent_brow, const int32_t* __restrict__ ent_slot,
@@ -121,13 +125,14 @@ __global__ __launch_bounds__(256) void vcsr_tile_kernel(
     float* __restrict__ partials) {
     using V = typename VecT<VEC>::T;
     constexpr int S = 64 / LPE;                              // streams per wave
+    constexpr int RS = tile_slot_stride(R);                  // slots stored per entry
     constexpr int EMAX = tile_chunk_entries(R) * MERGE;      // entries per wave
     constexpr int PMAX = kTileChunkPieces * MERGE;           // pieces per wave
     constexpr int U = 8;                                     // loads per block
     __shared__ uint32_t s_brow[kWaves][EMAX];
     __shared__ uint8_t s_mask[kWaves][EMAX];
     __shared__ uint8_t s_bad[kWaves][PMAX];
-    __shared__ __align__(16) float s_val[kWaves][EMAX * R];
+    __shared__ __align__(16) float s_val[kWaves][EMAX * RS];
     __shared__ int4 s_piece[kWaves][PMAX + 2];
     __shared__ int32_t s_first[kWaves][S + 1];
 
@@ -149,13 +154,13 @@ __global__ __launch_bounds__(256) void vcsr_tile_kernel(
     const uint32_t row_bytes = (uint32_t)O * 4u;
     for (int32_t i = lane; i < ne; i += 64) {
         const int64_t e = (int64_t)e0 + i;
-        int32_t sl[R];
-        load_slots<R>(ent_slot + e * R, sl);
+        int32_t sl[RS];
+        load_slots<RS>(ent_slot + e * RS, sl);
         const uint32_t br = (uint32_t)ent_brow[e];
-        float a[R];
+        float a[RS];
         uint32_t m = 0;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int r = 0; r < RS; ++r) {
             a[r] = 0.f;
             if (sl[r] >= 0) {
                 a[r] = val[sl[r]];
@@ -164,7 +169,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_kernel(
         }
         lb[i] = BUF ? (m ? br * row_bytes : kNoRow) : br;
         lm[i] = (uint8_t)m;
-        store_vals<R>(lv + i * R, a);
+        store_vals<RS>(lv + i * RS, a);
     }
     for (int32_t j = lane; j < np; j += 64) {
         int4 pc = pieces[p0 + j];
@@ -196,8 +201,8 @@ __global__ __launch_bounds__(256) void vcsr_tile_kernel(
     // (0 * inf = NaN) shows up as a non-finite row sum at the store, and the
     // piece is then recomputed with the presence bits (redo_piece).
     auto apply = [&](V (&acc)[R], int32_t tc, bool ok, const V& b) {
-        float a[R];
-        load_vals<R>(lv + tc * R, a);
+        float a[RS];
+        load_vals<RS>(lv + tc * RS, a);
 #pragma unroll
         for (int r = 0; r < R; ++r) fma_vec(acc[r], ok ? a[r] : 0.f, b);
     };
@@ -234,8 +239,8 @@ __global__ __launch_bounds__(256) void vcsr_tile_kernel(
         for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
         for (int32_t t = lp[q].z; t < lp[q + 1].z; ++t) {
             const V b = load_b(t, true, koff);
-            float a[R];
-            load_vals<R>(lv + t * R, a);
+            float a[RS];
+            load_vals<RS>(lv + t * RS, a);
             const uint32_t m = lm[t];
 #pragma unroll
             for (int r = 0; r < R; ++r)
@@ -372,28 +377,54 @@ __global__ __launch_bounds__(256) void vcsr_tile_kernel(
     }
 }
 
-// Adds the piece partials of every row of a split tile into C (one wave per
-// row and 64*VEC-column tile).  split: {row, first partial row, stride, pieces}.
+// Adds the piece partials of one row of a split tile into C; one block per
+// row.  split: {row, first partial row, stride, pieces}.  The block's 256
+// threads are `groups` groups of `cl` lanes: lane c of group g sums column
+// vector c of partials g, g + groups, ... (four loads in flight), and the
+// groups are then added in LDS, so a row split into many pieces costs a few
+// load latencies instead of one per piece.
 template <int VEC>
-__global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t n_units, int32_t nkt, int32_t O,
-                                                        int32_t accumulate,
+__global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t O, int32_t accumulate,
                                                         const int4* __restrict__ split,
                                                         const float* __restrict__ partials,
                                                         float* __restrict__ C) {
     using V = typename VecT<VEC>::T;
-    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-    const int32_t unit = (int32_t)(blockIdx.x * kWaves) + wave;
-    if (unit >= n_units) return;
-    const int32_t item = unit / nkt, kt = unit - item * nkt;
-    const int4 s = split[item];
-    const int32_t k = kt * 64 * VEC + lane * VEC;
-    if (k >= O) return;
-    V acc = zero_vec(V());
-    for (int32_t j = 0; j < s.w; ++j)
-        acc = add_vec(acc, *reinterpret_cast<const V*>(
-                               partials + (int64_t)(s.y + (int64_t)j * s.z) * O + k));
-    V* dst = reinterpret_cast<V*>(C + (int64_t)s.x * O + k);
-    *dst = accumulate ? add_vec(*dst, acc) : acc;
+    __shared__ V red[256];
+    const int4 s = split[blockIdx.x];
+    const int32_t nvec = (O + VEC - 1) / VEC;
+    int32_t cl = 1;
+    while (cl < nvec && cl < 64) cl <<= 1;
+    const int32_t groups = 256 / cl;
+    const int32_t tid = (int32_t)threadIdx.x, c = tid % cl, g = tid / cl;
+    const int64_t step = (int64_t)s.z * O;
+    auto part = [&](int32_t j, int32_t cv) {
+        return *reinterpret_cast<const V*>(partials + (int64_t)s.y * O + (int64_t)j * step +
+                                           (int64_t)cv * VEC);
+    };
+    for (int32_t c0 = 0; c0 < nvec; c0 += cl) {
+        const int32_t cv = c0 + c;
+        V acc = zero_vec(V());
+        if (cv < nvec) {
+            int32_t j = g;
+            for (; j + 3 * groups < s.w; j += 4 * groups) {
+                const V x0 = part(j, cv), x1 = part(j + groups, cv);
+                const V x2 = part(j + 2 * groups, cv), x3 = part(j + 3 * groups, cv);
+                acc = add_vec(acc, add_vec(add_vec(x0, x1), add_vec(x2, x3)));
+            }
+            for (; j < s.w; j += groups) acc = add_vec(acc, part(j, cv));
+        }
+        red[tid] = acc;
+        __syncthreads();
+        for (int32_t h = groups / 2; h >= 1; h >>= 1) {
+            if (g < h) red[tid] = add_vec(red[tid], red[tid + h * cl]);
+            __syncthreads();
+        }
+        if (g == 0 && cv < nvec) {
+            V* dst = reinterpret_cast<V*>(C + (int64_t)s.x * O + (int64_t)cv * VEC);
+            *dst = accumulate ? add_vec(*dst, red[tid]) : red[tid];
+        }
+        __syncthreads();
+    }
 }
 
 template <int VEC, int LPE, int R, bool BUF>
@@ -439,6 +470,7 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
         switch (d.tv_R) {
             case 1: e = launch_r<VEC, 1>(d, B, O, C, accumulate, b_bytes, st); break;
             case 2: e = launch_r<VEC, 2>(d, B, O, C, accumulate, b_bytes, st); break;
+            case 3: e = launch_r<VEC, 3>(d, B, O, C, accumulate, b_bytes, st); break;
             case 4: e = launch_r<VEC, 4>(d, B, O, C, accumulate, b_bytes, st); break;
             case 8: e = launch_r<VEC, 8>(d, B, O, C, accumulate, b_bytes, st); break;
             default: return hipErrorInvalidValue;
@@ -446,12 +478,9 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
         if (e != hipSuccess) return e;
     }
     if (d.tv_n_split > 0) {
-        const int32_t nkt = (O + 64 * VEC - 1) / (64 * VEC);
-        const int64_t ru = (int64_t)d.tv_n_split * nkt;
-        if (ru > INT32_MAX) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(vcsr_tile_reduce<VEC>, dim3((unsigned)((ru + kWaves - 1) / kWaves)),
-                           dim3(64 * kWaves), 0, st, (int32_t)ru, nkt, O, accumulate,
-                           reinterpret_cast<const int4*>(d.tv_split), d.partials, C);
+        hipLaunchKernelGGL(vcsr_tile_reduce<VEC>, dim3((unsigned)d.tv_n_split), dim3(256), 0, st,
+                           O, accumulate, reinterpret_cast<const int4*>(d.tv_split), d.partials,
+                           C);
         return hipGetLastError();
     }
     return hipSuccess;

@@ -149,8 +149,8 @@ std::vector<Tile> make_tiles(const RowLists& rl, int32_t M, int32_t cap, int nth
 }  // namespace
 
 TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
-    if (R != 0 && R != 1 && R != 2 && R != 4 && R != 8)
-        throw Error(kEinval, "tile height must be 0, 1, 2, 4 or 8");
+    if (R != 0 && R != 1 && R != 2 && R != 3 && R != 4 && R != 8)
+        throw Error(kEinval, "tile height must be 0, 1, 2, 3, 4 or 8");
     if (nthreads <= 0) nthreads = default_threads();
     const int32_t M = v.M;
     const RowLists rl = row_lists(v, nthreads);
@@ -160,7 +160,7 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
     std::vector<Tile> tiles;
     if (R == 0) {
         double best = 0;
-        for (int32_t cap : {1, 2, 4, 8}) {
+        for (int32_t cap : {1, 2, 3, 4, 8}) {
             std::vector<Tile> t = make_tiles(rl, M, cap, nthreads);
             int64_t ent = 0;
             for (const Tile& x : t) ent += x.nent;
@@ -185,7 +185,8 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
     const int64_t E = eoff.back();
     if (E > INT32_MAX) throw Error(kErange, "tile view has too many entries");
     tv.brow.resize((size_t)E);
-    tv.slot.assign((size_t)E * (size_t)R, -1);
+    const size_t stride = (size_t)tile_slot_stride(R);
+    tv.slot.assign((size_t)E * stride, -1);
     parallel_for((int64_t)tiles.size(), 1024, nthreads, [&](int64_t tb, int64_t te) {
         std::vector<int32_t> u, w;
         for (int64_t t = tb; t < te; ++t) {
@@ -207,7 +208,7 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
                 const int64_t pe = rl.ptr[(size_t)(x.row0 + r) + 1];
                 for (size_t q = 0; q < u.size() && p < pe; ++q) {
                     if (rl.col[(size_t)p] == u[q]) {
-                        tv.slot[((size_t)e0 + q) * (size_t)R + (size_t)r] = rl.slot[(size_t)p];
+                        tv.slot[((size_t)e0 + q) * stride + (size_t)r] = rl.slot[(size_t)p];
                         ++p;
                     }
                 }

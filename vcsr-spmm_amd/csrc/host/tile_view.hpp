@@ -21,6 +21,9 @@ namespace vcsr {
 // flight when each entry is a long B-row slice; for narrow B the kernel
 // merges several consecutive items per wave.
 constexpr int32_t tile_chunk_entries(int32_t R) { return R >= 8 ? 256 : 128; }
+// Slot indices stored per entry for tile height R (a power of two, so that
+// an entry's slots and staged values are one aligned vector).
+constexpr int32_t tile_slot_stride(int32_t R) { return R <= 2 ? R : (R <= 4 ? 4 : 8); }
 // Tile pieces per work item.
 constexpr int32_t kTileChunkPieces = 32;
 // Rows are cut into tiles inside fixed blocks of this many rows (so that
@@ -29,7 +32,7 @@ constexpr int32_t kTileChunkPieces = 32;
 constexpr int32_t kTileRowBlock = 4096;
 
 struct TileView {
-    int32_t R = 1;                // accumulator rows per tile: 1, 2, 4 or 8
+    int32_t R = 1;                // accumulator rows per tile: 1, 2, 3, 4 or 8
     int32_t n_tiles = 0;
     // Work items, 4 ints each: first entry, end entry, first piece, end piece.
     std::vector<int32_t> chunks;
@@ -37,7 +40,8 @@ struct TileView {
     // first partial row (pieces of a split tile) or -1 (the piece writes C).
     std::vector<int32_t> pieces;
     std::vector<int32_t> brow;    // per entry: B row = segment base + local column
-    std::vector<int32_t> slot;    // R per entry: VCSR slot for tile row r, or -1
+    // tile_slot_stride(R) per entry: VCSR slot for tile row r, or -1.
+    std::vector<int32_t> slot;
     // Rows of split tiles, 4 ints each: row, first partial row, stride
     // between the piece partials of that row, piece count.
     std::vector<int32_t> split;
@@ -46,7 +50,7 @@ struct TileView {
 };
 
 // Builds the view.  R = 0 picks the tile height that minimises the modelled
-// cost (B-row loads plus accumulator updates); R = 1, 2, 4 or 8 forces it.
+// cost (B-row loads plus accumulator updates); R = 1, 2, 3, 4 or 8 forces it.
 TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads);
 
 }  // namespace vcsr
