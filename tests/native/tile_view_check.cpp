@@ -1,0 +1,168 @@
+// tile_view_check.cpp - CPU checks of the row-tile view (host/tile_view.cpp)
+// that the tile-stationary kernel walks.  Built and run by
+// tests/test_tile_view.py against the library's host objects.
+//
+// For every matrix and tile height the view must
+//  * hold exactly the CSR nonzeros: each (tile row, entry) slot that is not
+//    -1 names a VCSR slot whose value and column (entry's B row) are one
+//    nonzero of that row, and the multiset of those equals the CSR's;
+//  * cover every row once: by a piece writing C, or as a split-tile row;
+//  * chain its work items and pieces contiguously within the LDS limits the
+//    kernel is compiled for (entries per item, pieces per item, rows per
+//    piece);
+//  * keep each tile's entries sorted by column (the B rows are walked in
+//    the order of the row's nonzeros).
+// Exit status 0 and "ALL OK" when every case passes.
+#include <algorithm>
+#include <cstdio>
+#include <tuple>
+#include <vector>
+
+#include "../../vcsr-spmm_amd/csrc/host/core.hpp"
+#include "../../vcsr-spmm_amd/csrc/host/tile_view.hpp"
+
+using namespace vcsr;
+
+static int fail(const char* what, int M, int R) {
+    std::printf("FAIL %s (M=%d R=%d)\n", what, M, R);
+    return 1;
+}
+
+static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, int expect_R) {
+    const Vcsr v = build_vcsr(csr, segw, bundle, layout, 2);
+    const TileView tv = make_tile_view(v, R_req, 2);
+    const int R = tv.R, RS = tile_slot_stride(R), M = csr.M;
+    if (expect_R > 0 && R != expect_R) return fail("tile height", M, R);
+    const int64_t E = tv.n_entries();
+    if ((int64_t)tv.slot.size() != E * RS) return fail("slot array size", M, R);
+    const int nc = (int)tv.chunks.size() / 4, np = (int)tv.pieces.size() / 4;
+    const int cap = tile_chunk_entries(R);
+    int64_t prev_e = 0;
+    int prev_p = 0;
+    for (int c = 0; c < nc; ++c) {
+        const int e0 = tv.chunks[4 * c], e1 = tv.chunks[4 * c + 1];
+        const int p0 = tv.chunks[4 * c + 2], p1 = tv.chunks[4 * c + 3];
+        if (e0 != prev_e || p0 != prev_p) return fail("items not contiguous", M, R);
+        if (e1 - e0 < 1 || e1 - e0 > cap) return fail("item entry count", M, R);
+        if (p1 - p0 < 1 || p1 - p0 > kTileChunkPieces) return fail("item piece count", M, R);
+        if (tv.pieces[4 * p0 + 2] != e0) return fail("item's first piece", M, R);
+        for (int p = p0; p < p1; ++p) {
+            const int pe = p + 1 < p1 ? tv.pieces[4 * (p + 1) + 2] : e1;
+            if (pe - tv.pieces[4 * p + 2] < 1) return fail("empty piece", M, R);
+            if (tv.pieces[4 * p + 1] < 1 || tv.pieces[4 * p + 1] > R) return fail("piece rows", M, R);
+        }
+        prev_e = e1;
+        prev_p = p1;
+    }
+    if (prev_e != E || prev_p != np) return fail("items do not cover the view", M, R);
+
+    std::vector<std::tuple<int, int, float>> want, got;
+    for (int r = 0; r < M; ++r)
+        for (int p = csr.row_ptr[r]; p < csr.row_ptr[r + 1]; ++p)
+            want.emplace_back(r, csr.col[p], csr.val[p]);
+    std::vector<int> covered((size_t)M, 0);
+    for (int p = 0; p < np; ++p) {
+        const int row0 = tv.pieces[4 * p], nr = tv.pieces[4 * p + 1], b = tv.pieces[4 * p + 2];
+        const int e = p + 1 < np ? tv.pieces[4 * (p + 1) + 2] : (int)E;
+        for (int q = b; q < e; ++q) {
+            if (q > b && tv.brow[q] < tv.brow[q - 1]) return fail("entries not in column order", M, R);
+            for (int r = 0; r < RS; ++r) {
+                const int s = tv.slot[(size_t)q * RS + r];
+                if (s < 0) continue;
+                if (r >= nr) return fail("slot beyond the tile's rows", M, R);
+                if (s >= (int)v.lcol.size() || v.lcol[s] < 0) return fail("slot is padding", M, R);
+                got.emplace_back(row0 + r, tv.brow[q], v.val[s]);
+            }
+        }
+        if (tv.pieces[4 * p + 3] < 0)
+            for (int r = 0; r < nr; ++r) covered[(size_t)(row0 + r)]++;
+    }
+    for (size_t i = 0; i < tv.split.size() / 4; ++i) {
+        covered[(size_t)tv.split[4 * i]]++;
+        const int q = tv.split[4 * i + 1], stride = tv.split[4 * i + 2], n = tv.split[4 * i + 3];
+        if (n < 2 || q < 0 || (int64_t)q + (int64_t)(n - 1) * stride >= tv.n_partial_rows)
+            return fail("split row partials out of range", M, R);
+    }
+    for (int r = 0; r < M; ++r)
+        if (covered[(size_t)r] != 1) return fail("row not covered exactly once", M, R);
+    std::sort(want.begin(), want.end());
+    std::sort(got.begin(), got.end());
+    if (want != got) return fail("nonzeros differ from the CSR", M, R);
+    std::printf("ok M=%d nnz=%d layout=%d R=%d entries=%lld items=%d pieces=%d split_rows=%zu\n", M,
+                csr.nnz, layout, R, (long long)E, nc, np, tv.split.size() / 4);
+    return 0;
+}
+
+// Block rows of height bh with `blocks` random bh x bw blocks each; an entry
+// is kept with probability keep_pct %.  Duplicate columns in a row appear
+// when dup is set.
+static Csr block_matrix(uint64_t seed, int nbr, int bh, int N, int blocks, int bw, int keep_pct,
+                        bool dup) {
+    Coo c;
+    c.M = nbr * bh;
+    c.N = N;
+    uint64_t x = seed * 0x9E3779B97F4A7C15ULL + 1;
+    auto next = [&]() {
+        x ^= x >> 12;
+        x ^= x << 25;
+        x ^= x >> 27;
+        return x * 0x2545F4914F6CDD1DULL;
+    };
+    const int nbc = std::max(1, N / bw);
+    for (int br = 0; br < nbr; ++br)
+        for (int k = 0; k < blocks; ++k) {
+            const int bc = (int)(next() % (uint64_t)nbc);
+            for (int i = 0; i < bh; ++i)
+                for (int j = 0; j < bw; ++j) {
+                    if ((int)(next() % 100) >= keep_pct) continue;
+                    const int col = bc * bw + j;
+                    if (col >= N) continue;
+                    c.rows.push_back(br * bh + i);
+                    c.cols.push_back(col);
+                    c.vals.push_back((float)((int)(next() % 2001) - 1000) / 512.f);
+                    if (dup && next() % 13 == 0) {
+                        c.rows.push_back(br * bh + i);
+                        c.cols.push_back(col);
+                        c.vals.push_back(0.75f);
+                    }
+                }
+        }
+    return coo_to_csr(c);
+}
+
+int main() {
+    int bad = 0;
+    const Csr cfg1 = coo_to_csr(gen_coo(1, 0));
+    bad |= check(cfg1, 4, 64, kLayoutS, 0, 1);  // random columns: no shared rows
+    bad |= check(cfg1, 4, 64, kLayoutH, 2, 2);
+    bad |= check(cfg1, 4, 64, kLayoutS, 8, 8);
+    // Block rows: the automatic height follows the block height.
+    bad |= check(block_matrix(1, 50, 3, 600, 9, 3, 100, false), 4, 64, kLayoutS, 0, 3);
+    bad |= check(block_matrix(2, 40, 2, 500, 9, 3, 100, false), 4, 64, kLayoutS, 0, 2);
+    bad |= check(block_matrix(3, 20, 8, 700, 9, 4, 100, false), 4, 64, kLayoutS, 0, 8);
+    bad |= check(block_matrix(4, 30, 4, 400, 9, 3, 100, false), 8, 32, kLayoutH, 0, 4);
+    // Partial blocks, duplicates, every forced height, every layout.
+    for (int R : {1, 2, 3, 4, 8})
+        for (int layout : {kLayoutH, kLayoutS, kLayoutTC}) {
+            const Csr a = block_matrix(10 + R, 30, 3, 300, 7, 3, 75, true);
+            bad |= check(a, 4, 64, layout, R, R);
+        }
+    // Tiles wider than one work item (split into pieces with partial sums).
+    for (int R : {1, 3, 8}) bad |= check(block_matrix(20 + R, 6, 8, 4096, 300, 4, 90, false), 4, 64, kLayoutS, R, R);
+    // Empty rows and an empty matrix.
+    {
+        Coo c;
+        c.M = 9;
+        c.N = 5;
+        c.rows = {2, 2, 6};
+        c.cols = {0, 4, 4};
+        c.vals = {1.f, 2.f, 3.f};
+        for (int R : {0, 1, 2, 4}) bad |= check(coo_to_csr(c), 4, 64, kLayoutS, R, R ? R : 0);
+        Coo z;
+        z.M = 7;
+        z.N = 3;
+        bad |= check(coo_to_csr(z), 4, 64, kLayoutS, 0, 0);
+    }
+    std::printf(bad ? "FAILED\n" : "ALL OK\n");
+    return bad;
+}
