@@ -225,7 +225,7 @@ void vcsr_tile_kernel(
             if (r >= pc.y) break;
             if (pc.w < 0) {
                 V* dst = reinterpret_cast<V*>(C + (int64_t)(pc.x + r) * O + k);
-                *dst = accumulate ? add_vec(*dst, acc[r]) : acc[r];
+                store_nt(dst, accumulate ? add_vec(*dst, acc[r]) : acc[r]);
             } else {
                 *reinterpret_cast<V*>(partials + (int64_t)(pc.w + r) * O + k) = acc[r];
             }

@@ -52,6 +52,18 @@ __device__ __forceinline__ float4 shfl_xor_vec(float4 x, int m) {
                        __shfl_xor(x.w, m));
 }
 
+// Non-temporal stores (written once, not read again by this kernel): they do
+// not displace B rows from L2.
+typedef float nt_float2 __attribute__((ext_vector_type(2)));
+typedef float nt_float4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_nt(float* p, float x) { __builtin_nontemporal_store(x, p); }
+__device__ __forceinline__ void store_nt(float2* p, float2 x) {
+    __builtin_nontemporal_store(__builtin_bit_cast(nt_float2, x), reinterpret_cast<nt_float2*>(p));
+}
+__device__ __forceinline__ void store_nt(float4* p, float4 x) {
+    __builtin_nontemporal_store(__builtin_bit_cast(nt_float4, x), reinterpret_cast<nt_float4*>(p));
+}
+
 // gfx9 raw buffer resource flags: 32-bit data, no swizzle.  Loads past the
 // record count return zeros instead of faulting.
 constexpr int32_t kRawBufferFlags = 0x00020000;
