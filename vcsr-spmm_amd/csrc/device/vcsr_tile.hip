@@ -136,7 +136,9 @@ void vcsr_tile_kernel(
     __shared__ int4 s_piece[kWaves][PMAX + 2];
     __shared__ int32_t s_first[kWaves][S + 1];
 
-    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+    // Wave-uniform indices, so the work-item records are scalar loads.
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63);
     const int32_t w = (int32_t)(xcd_remap(blockIdx.x, gridDim.x) * kWaves) + wave;
     const int32_t c0 = w * MERGE;
     if (c0 >= n_chunks) return;
@@ -162,7 +164,7 @@ void vcsr_tile_kernel(
 #pragma unroll
         for (int r = 0; r < RS; ++r) {
             a[r] = 0.f;
-            if (sl[r] >= 0) {
+            if (r < R && sl[r] >= 0) {  // slots past R are always -1
                 a[r] = val[sl[r]];
                 m |= 1u << r;
             }
