@@ -29,6 +29,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_FP32_PEAK_TFS = 157.3  # dense FP32 MFMA, MI355X
 
 CONFIGS = {
     # name: (cfg, O, segw, bundle, tileK, layout, B distribution)
@@ -252,6 +253,17 @@ def main():
                      "traffic": measured_traffic(args.config, args.algo),
                      "bytes_alg": bytes_alg},
     }
+    if args.algo == "mfma":
+        # Matrix-core utilisation: issued MFMA FLOPs (dense group tiles,
+        # padding included) per kernel time against the dense FP32 MFMA peak,
+        # and the useful share of the issued FLOPs.
+        ops, fpo = vs.mfma_work(fmt, O, tileK)
+        issued = float(ops) * fpo
+        rate = issued / (kernel_ms * 1e-3) / 1e12
+        out["mfma"] = {"instructions": ops, "issued_gflop": round(issued / 1e9, 4),
+                       "useful_frac": round(flop / issued, 4) if issued else None,
+                       "tflops_issued": round(rate, 2), "peak_tflops": MFMA_FP32_PEAK_TFS,
+                       "utilization": round(rate / MFMA_FP32_PEAK_TFS, 4)}
     if not args.no_cpu_baseline:
         gf, reps, secs = cpu_baseline(orc, csr, B, args.cpu_seconds)
         out["cpu_baseline"] = {"value": round(gf, 3), "unit": "GFLOP/s", "cores": 1,

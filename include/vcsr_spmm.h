@@ -210,6 +210,15 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
 int spmm_vcsr_mfma(const vcsr_fmt* fmt, const float* dB, int32_t O,
                    float* dC, void* stream, float* ms);
 
+/* Work of the FP32-MFMA kernel for one SpMM of width O with column tile
+ * tileK (0 as spmm_vcsr_mfma uses): the MFMA instructions it issues (every
+ * group as a dense tile, padding included) and the FLOPs of each.  For
+ * reporting MFMA utilisation: useful fraction = 2*nnz*O / (ops*flops_per_op),
+ * achieved rate = ops*flops_per_op / time against the FP32 MFMA peak.
+ * Host only (no upload needed).  No reference counterpart. */
+int vcsr_mfma_work(const vcsr_fmt* fmt, int32_t O, int32_t tileK, int64_t* ops,
+                   int32_t* flops_per_op);
+
 /* CPU CSR SpMM, C = A*B in FP32, for each row: p ascending, k inner, one
  * fused multiply-add per term (the loop order of src/kernels.cu:25-32).
  * nthreads <= 0 uses every hardware thread (rows are independent, so the

@@ -262,3 +262,35 @@ def test_cpu_spmm_matches_oracle_bitwise(vs, orc, threads):
     C = vs.spmm_csr_cpu(csr, B, threads)
     ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
     assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))
+
+
+# --------------------------------------------------- MFMA work accounting
+def test_mfma_work_dense_blocks_are_fully_used(vs):
+    """cfg5 in layout TC: every group is one dense 16x16 block, so the
+    16x16x4 MFMAs the kernel issues carry exactly 2*nnz*O useful FLOPs when O
+    is a multiple of the kernel's column tile (16 x up to 8 blocks), and the
+    tail tile's padding otherwise (O=520: 5 tiles of 128 columns)."""
+    csr = vs.coo_to_csr(vs.generate_coo(5, 0))
+    fmt = vs.build_vcsr(csr, 16, 16, vs.LAYOUT_TC)
+    for O, issued_cols in ((16, 16), (512, 512), (520, 640)):
+        ops, fpo = vs.mfma_work(fmt, O)
+        assert fpo == 2 * 16 * 16 * 4
+        assert ops * fpo == 2 * csr.nnz * issued_cols
+
+
+def test_mfma_work_counts_padding(vs):
+    """bundle 64 (32x32x2 tiles): a group of n active lanes issues
+    ceil(n/32) row blocks x ceil(segw/2) K-steps x the column blocks of
+    ceil(O/kw) column tiles (tileK=64: kw = 64 columns = 2 blocks; O=70 -> 4)."""
+    rng = np.random.default_rng(2)
+    rows, cols, vals = random_csr(rng, 300, 97, density=0.04)
+    csr = product_csr(vs, 300, 97, rows, cols, vals)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    a = fmt.arrays()
+    nact = [(a["lcol"][a["group_ptr"][g]:a["group_ptr"][g] + 64] >= 0).sum()
+            for g in range(fmt.num_groups)]
+    O = 70
+    ops, fpo = vs.mfma_work(fmt, O, 64)
+    assert fpo == 2 * 32 * 32 * 2
+    assert ops == sum(-(-n // 32) for n in nact) * 2 * 4
+    assert ops * fpo >= 2 * csr.nnz * O

@@ -41,7 +41,8 @@ EXPORTS = (
     "vcsr_last_error vcsr_version vcsr_mtx_read vcsr_coo_create vcsr_coo_view_get "
     "vcsr_coo_free vcsr_gen_coo vcsr_gen_dense vcsr_coo_to_csr vcsr_csr_create "
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
-    "vcsr_fmt_set_tile_rows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_vcsr spmm_vcsr_ex spmm_vcsr_mfma spmm_csr_cpu "
+    "vcsr_fmt_set_tile_rows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_vcsr "
+    "spmm_vcsr_ex spmm_vcsr_mfma vcsr_mfma_work spmm_csr_cpu "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
     "vcsr_memcpy_d2h vcsr_memcpy_d2d vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
     "vcsr_stream_sync vcsr_device_sync vcsr_event_create vcsr_event_destroy "
@@ -113,6 +114,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "spmm_vcsr": (C.c_int, [P, P, I32, I32, P, P, pF]),
         "spmm_vcsr_ex": (C.c_int, [P, P, I32, I32, P, P, pF, I32, I32]),
         "spmm_vcsr_mfma": (C.c_int, [P, P, I32, P, P, pF]),
+        "vcsr_mfma_work": (C.c_int, [P, I32, I32, C.POINTER(I64), pI]),
         "spmm_csr_cpu": (C.c_int, [I32, P, P, P, P, I32, P, I32]),
         "vcsr_device_count": (C.c_int, [pI]),
         "vcsr_device_name": (C.c_int, [C.c_char_p, I32]),
@@ -427,6 +429,14 @@ def run_vcsr_tc_spmm_gpu(fmt: Vcsr, dB, O, dC, stream=None, timed=False):
 
 
 run_vcsr_mfma_spmm_gpu = run_vcsr_tc_spmm_gpu
+
+
+def mfma_work(fmt: Vcsr, O: int, tileK: int = 0) -> tuple[int, int]:
+    """(MFMA instructions, FLOPs per instruction) the FP32-MFMA kernel issues
+    for one SpMM of width O (host only)."""
+    ops, fpo = C.c_int64(), C.c_int32()
+    _check(load_library().vcsr_mfma_work(fmt._h, O, tileK, C.byref(ops), C.byref(fpo)))
+    return ops.value, fpo.value
 
 
 def run_vcsr_spmm_gpu_ex(fmt: Vcsr, dB, O, tileK, dC, stream=None, timed=False,

@@ -290,6 +290,21 @@ int main(int argc, char** argv) {
         }
         report_check(label);
         report_roofline(sum / o.repeat);
+        if (mfma) {
+            // Utilisation of the matrix cores: useful FLOPs over issued MFMA
+            // FLOPs (padding of the dense group tiles), and the issued rate
+            // over the dense FP32 MFMA peak of MI355X (157.3 TFLOP/s).
+            int64_t ops = 0;
+            int32_t fpo = 0;
+            CHECK(vcsr_mfma_work(fmt, O, 0, &ops, &fpo));
+            const double issued = (double)ops * fpo;
+            const double rate = issued / ((sum / o.repeat) * 1e-3) / 1e12;
+            std::printf("mfma: %lld instructions, %.3f GFLOP issued, useful %.1f%%, "
+                        "%.2f TFLOP/s issued = %.2f%% of 157.3 TFLOP/s FP32 MFMA peak\n",
+                        (long long)ops, issued / 1e9,
+                        issued > 0 ? 100.0 * 2.0 * A.nnz * O / issued : 0.0, rate,
+                        100.0 * rate / 157.3);
+        }
         std::printf("%-12s%8.3f ms %9.2f GFLOP/s  [segw=%d,bundle=%d,tileK=%d,groups=%d]\n", label,
                     sum / o.repeat, gflops(sum / o.repeat), v.segw, v.bundle, o.tileK,
                     v.num_groups);

@@ -27,6 +27,14 @@ hipError_t launch_vcsr_mfma(const Vcsr& v, const DeviceFmt& d, const float* B, i
 // Column-block width (in 32-column MFMA blocks) used for a tileK request.
 int mfma_col_blocks(int32_t tileK, int32_t O);
 
+// MFMA instructions launch_vcsr_mfma issues for one SpMM (padding of the
+// dense tiles included) and the FLOPs of each.
+struct MfmaWork {
+    int64_t ops = 0;
+    int32_t flops_per_op = 0;
+};
+MfmaWork mfma_work(const Vcsr& v, int32_t O, int32_t tileK);
+
 // vcsr_rowmajor.hip: row-stationary traversal of the VCSR slots; C = A*B
 // (accumulate = 0) or C += A*B (accumulate = 1).  Needs d.partials sized for
 // O when the format has split rows.

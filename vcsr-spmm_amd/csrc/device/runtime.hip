@@ -352,6 +352,17 @@ int spmm_vcsr_mfma(const vcsr_fmt* fmt, const float* dB, int32_t O, float* dC, v
     return spmm_vcsr_ex(fmt, dB, O, 0, dC, stream, ms, VCSR_KERNEL_MFMA, 1);
 }
 
+int vcsr_mfma_work(const vcsr_fmt* fmt, int32_t O, int32_t tileK, int64_t* ops,
+                   int32_t* flops_per_op) {
+    return guarded([&] {
+        need(fmt && ops && flops_per_op, "null argument");
+        need(O >= 0, "negative O");
+        const vcsr::MfmaWork w = vcsr::mfma_work(fmt->v, O, tileK);
+        *ops = w.ops;
+        *flops_per_op = w.flops_per_op;
+    });
+}
+
 int vcsr_device_count(int32_t* n) {
     return guarded([&] {
         need(n != nullptr, "null output");

@@ -229,27 +229,67 @@ int mfma_col_blocks(int32_t tileK, int32_t O) {
     return pow2_at_most(std::max(1, c), 8);
 }
 
+namespace {
+
+// Tile shape the launcher uses: 16x16x4 tiles for bundle <= 16, else
+// 32x32x2; ks K-steps per pass, ncb column blocks per wave.
+struct MfmaShape {
+    bool m16;
+    int ks, ncb;
+    int32_t tile() const { return m16 ? 16 : 32; }   // rows = columns of a tile
+    int32_t kstep() const { return m16 ? 4 : 2; }    // segment columns per MFMA
+};
+
+MfmaShape mfma_shape(const Vcsr& v, int32_t O, int32_t tileK) {
+    MfmaShape s;
+    s.m16 = v.bundle <= 16;
+    if (s.m16) {
+        const int32_t want = tileK > 0 ? tileK : 128;
+        s.ncb = pow2_at_most(std::max(1, (std::min(want, std::max<int32_t>(O, 1)) + 15) / 16), 8);
+        s.ks = v.segw <= 4 ? 1 : (v.segw <= 8 ? 2 : 4);
+    } else {
+        s.ncb = mfma_col_blocks(tileK, O);
+        s.ks = v.segw <= 2 ? 1 : (v.segw <= 4 ? 2 : (v.segw <= 8 ? 4 : 8));
+    }
+    return s;
+}
+
+}  // namespace
+
+MfmaWork mfma_work(const Vcsr& v, int32_t O, int32_t tileK) {
+    MfmaWork w;
+    if (O <= 0 || v.M == 0) return w;
+    const MfmaShape s = mfma_shape(v, O, tileK);
+    const int32_t tile = s.tile(), kw = tile * s.ncb;
+    const int64_t passes = (v.segw + s.kstep() * s.ks - 1) / (s.kstep() * s.ks);
+    const int64_t colblocks = (int64_t)((O + kw - 1) / kw) * s.ncb;
+    int64_t lane_blocks = 0;  // sum over groups of ceil(active lanes / tile)
+    for (int32_t g = 0; g < v.num_groups(); ++g) {
+        int32_t nact = 0;
+        for (int32_t l = 0; l < v.bundle; ++l) nact += v.lcol[(size_t)v.group_ptr[g] + l] >= 0;
+        lane_blocks += (nact + tile - 1) / tile;
+    }
+    w.ops = lane_blocks * passes * s.ks * colblocks;
+    w.flops_per_op = 2 * tile * tile * s.kstep();
+    return w;
+}
+
 hipError_t launch_vcsr_mfma(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                             int32_t tileK, float* C, hipStream_t st) {
     if (d.n_items == 0 || O <= 0 || v.M == 0) return hipSuccess;
+    const MfmaShape s = mfma_shape(v, O, tileK);
     KernelFn fn;
-    int32_t kw;
-    if (v.bundle <= 16) {
-        const int32_t want = tileK > 0 ? tileK : 128;
-        const int ncb =
-            pow2_at_most(std::max(1, (std::min(want, std::max<int32_t>(O, 1)) + 15) / 16), 8);
-        kw = 16 * ncb;
-        if (v.segw <= 4) fn = pick16<1>(ncb);
-        else if (v.segw <= 8) fn = pick16<2>(ncb);
-        else fn = pick16<4>(ncb);
+    if (s.m16) {
+        if (s.ks == 1) fn = pick16<1>(s.ncb);
+        else if (s.ks == 2) fn = pick16<2>(s.ncb);
+        else fn = pick16<4>(s.ncb);
     } else {
-        const int ncb = mfma_col_blocks(tileK, O);
-        kw = 32 * ncb;
-        if (v.segw <= 2) fn = pick32<1>(ncb);
-        else if (v.segw <= 4) fn = pick32<2>(ncb);
-        else if (v.segw <= 8) fn = pick32<4>(ncb);
-        else fn = pick32<8>(ncb);
+        if (s.ks == 1) fn = pick32<1>(s.ncb);
+        else if (s.ks == 2) fn = pick32<2>(s.ncb);
+        else if (s.ks == 4) fn = pick32<4>(s.ncb);
+        else fn = pick32<8>(s.ncb);
     }
+    const int32_t kw = s.tile() * s.ncb;
     const int32_t nkt = (O + kw - 1) / kw;
     const int64_t units = (int64_t)d.n_items * nkt;
     if (units > INT32_MAX) return hipErrorInvalidValue;
