@@ -17,10 +17,13 @@
 
 namespace vcsr {
 
-// Entries of one work item, by tile height R.  Small items keep many waves in
-// flight when each entry is a long B-row slice; for narrow B the kernel
-// merges several consecutive items per wave.
-constexpr int32_t tile_chunk_entries(int32_t R) { return R >= 8 ? 256 : 128; }
+// Entries of one work item, by tile height R: 32 per tile row, measured best
+// on MI355X for R = 1 (16..128 tried, power-law rows), R = 3 (64..128, banded
+// 3x3 blocks: one tile per wave) and R = 8 (128..256).  Small items keep many
+// waves in flight and the rows a XCD works on close together (its L2 holds
+// their B rows); for narrow B the kernel merges several consecutive items
+// per wave.
+constexpr int32_t tile_chunk_entries(int32_t R) { return 32 * R; }
 // Slot indices stored per entry for tile height R (a power of two, so that
 // an entry's slots and staged values are one aligned vector).
 constexpr int32_t tile_slot_stride(int32_t R) { return R <= 2 ? R : (R <= 4 ? 4 : 8); }
