@@ -36,7 +36,7 @@ static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, in
     const int64_t E = tv.n_entries();
     if ((int64_t)tv.slot.size() != E * RS) return fail("slot array size", M, R);
     const int nc = (int)tv.chunks.size() / 4, np = (int)tv.pieces.size() / 4;
-    const int cap = tile_chunk_entries(R);
+    const int cap = tile_piece_entries(R);
     int64_t prev_e = 0;
     int prev_p = 0;
     for (int c = 0; c < nc; ++c) {

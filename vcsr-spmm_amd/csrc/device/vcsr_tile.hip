@@ -12,7 +12,7 @@
 // a row-stationary SpMM, by the block height.
 //
 // Work item (one wave): MERGE consecutive work items of the view, each a run
-// of tile pieces with at most tile_chunk_entries(R) entries
+// of tile pieces with at most tile_piece_entries(R) entries
 // (host/tile_view.hpp).
 // Phase 1 (lane per entry): read the entry's B row and R slot indices, gather
 // the R values from the VCSR value array and stage (B-row byte offset,
@@ -126,7 +126,7 @@ void vcsr_tile_kernel(
     using V = typename VecT<VEC>::T;
     constexpr int S = 64 / LPE;                              // streams per wave
     constexpr int RS = tile_slot_stride(R);                  // slots stored per entry
-    constexpr int EMAX = tile_chunk_entries(R) * MERGE;      // entries per wave
+    constexpr int EMAX = tile_piece_entries(R) * MERGE;      // entries per wave
     constexpr int PMAX = kTileChunkPieces * MERGE;           // pieces per wave
     constexpr int U = 8;                                     // loads per block
     __shared__ uint32_t s_brow[kWaves][EMAX];

@@ -217,9 +217,10 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
     });
 
     // Work items.  A tile longer than half a work item's entry budget gets
-    // work items of its own (cut into equal pieces that write partial sums
-    // when it exceeds the budget); shorter tiles are packed in row order.
-    const int32_t cap_e = tile_chunk_entries(R);
+    // work items of its own (cut into equal pieces of at most
+    // tile_piece_entries that write partial sums when it needs more than
+    // one); shorter tiles are packed in row order.
+    const int32_t cap_e = tile_chunk_entries(R), cap_p = tile_piece_entries(R);
     int64_t ce0 = 0, cent = 0;
     int32_t cp0 = 0;
     auto close_chunk = [&](int64_t next_e) {
@@ -236,7 +237,7 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
         const int64_t e0 = eoff[t];
         if (x.nent > cap_e / 2) {
             close_chunk(e0);
-            const int64_t npc = (x.nent + cap_e - 1) / cap_e;
+            const int64_t npc = (x.nent + cap_p - 1) / cap_p;
             const int64_t size = (x.nent + npc - 1) / npc;
             const int64_t base = n_partial;
             for (int64_t j = 0; j < npc; ++j) {

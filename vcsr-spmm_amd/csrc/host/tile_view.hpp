@@ -24,6 +24,12 @@ namespace vcsr {
 // their B rows); for narrow B the kernel merges several consecutive items
 // per wave.
 constexpr int32_t tile_chunk_entries(int32_t R) { return 32 * R; }
+// Entries of one piece of a tile longer than half a work item (it gets work
+// items of its own): at least 64, so a long row is cut into fewer pieces
+// (and partial rows for the reduce kernel); larger pieces unbalance the
+// streams when several work items share a wave (narrow B).  The kernel's
+// LDS list holds this many entries per merged work item.
+constexpr int32_t tile_piece_entries(int32_t R) { return 32 * R > 64 ? 32 * R : 64; }
 // Slot indices stored per entry for tile height R (a power of two, so that
 // an entry's slots and staged values are one aligned vector).
 constexpr int32_t tile_slot_stride(int32_t R) { return R <= 2 ? R : (R <= 4 ? 4 : 8); }
