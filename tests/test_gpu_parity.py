@@ -364,3 +364,24 @@ def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind):
     assert np.array_equal(np.isneginf(C), np.isneginf(ref)), kind
     fin = np.isfinite(ref)
     assert np.allclose(C[fin], ref[fin], rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("kind", ["row", "tile"])
+def test_b_of_2gb_or_more_uses_64bit_addresses(gpu, orc, st, kind):
+    """B of 2^31 bytes or more cannot be addressed with 32-bit buffer
+    offsets; the row and tile kernels then take their 64-bit-address path.
+    N = 2^19 + 3 rows of O = 1024 floats (2.0 GiB + 12 KiB), 3000 sparse rows
+    whose columns reach the last B rows."""
+    vs = gpu
+    rng = np.random.default_rng(21)
+    N, O, M = (1 << 19) + 3, 1024, 3000
+    nnz_row = 24
+    rows = np.repeat(np.arange(M, dtype=np.int32), nnz_row)
+    cols = rng.integers(0, N, size=M * nnz_row).astype(np.int32)
+    cols[:nnz_row] = N - 1 - np.arange(nnz_row)  # row 0 reads the end of B
+    vals = rng.uniform(-1, 1, size=M * nnz_row).astype(np.float32)
+    csr = vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
+    B = vs.gen_dense(77, 0, N, O)
+    assert B.nbytes >= 1 << 31
+    C = _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=128)
+    _rowsample_check(vs, orc, csr, B, C, 300, 21)
