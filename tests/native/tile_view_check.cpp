@@ -14,6 +14,8 @@
 //    the order of the row's nonzeros).
 // Exit status 0 and "ALL OK" when every case passes.
 #include <algorithm>
+#include <cmath>
+#include <cstring>
 #include <cstdio>
 #include <tuple>
 #include <vector>
@@ -35,6 +37,8 @@ static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, in
     if (expect_R > 0 && R != expect_R) return fail("tile height", M, R);
     const int64_t E = tv.n_entries();
     if ((int64_t)tv.slot.size() != E * RS) return fail("slot array size", M, R);
+    if ((int64_t)tv.val.size() != E * RS) return fail("value array size", M, R);
+    if ((int64_t)tv.mask.size() != E) return fail("mask array size", M, R);
     const int nc = (int)tv.chunks.size() / 4, np = (int)tv.pieces.size() / 4;
     const int cap = tile_piece_entries(R);
     int64_t prev_e = 0;
@@ -67,11 +71,20 @@ static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, in
         for (int q = b; q < e; ++q) {
             if (q > b && tv.brow[q] < tv.brow[q - 1]) return fail("entries not in column order", M, R);
             for (int r = 0; r < RS; ++r) {
+                // The kernel reads the values and presence bits; the slots
+                // say where those values come from.
                 const int s = tv.slot[(size_t)q * RS + r];
-                if (s < 0) continue;
+                const float a = tv.val[(size_t)q * RS + r];
+                const bool present = (tv.mask[q] >> r) & 1;
+                if (present != (s >= 0)) return fail("presence bit differs from slot", M, R);
+                if (s < 0) {
+                    if (a != 0.f || std::signbit(a)) return fail("absent value not +0", M, R);
+                    continue;
+                }
                 if (r >= nr) return fail("slot beyond the tile's rows", M, R);
                 if (s >= (int)v.lcol.size() || v.lcol[s] < 0) return fail("slot is padding", M, R);
-                got.emplace_back(row0 + r, tv.brow[q], v.val[s]);
+                if (std::memcmp(&a, &v.val[s], sizeof a) != 0) return fail("value differs from slot's", M, R);
+                got.emplace_back(row0 + r, tv.brow[q], a);
             }
         }
         if (tv.pieces[4 * p + 3] < 0)

@@ -209,7 +209,8 @@ void free_device_fmt(DeviceFmt& d) {
     for (void* p : {(void*)d.group_ptr, (void*)d.group_depth, (void*)d.group_seg_base,
                     (void*)d.group_rows, (void*)d.group_nact, (void*)d.lcol, (void*)d.val,
                     (void*)d.items, (void*)d.pair_rec, (void*)d.row_items, (void*)d.split_rows,
-                    (void*)d.tv_chunks, (void*)d.tv_pieces, (void*)d.tv_brow, (void*)d.tv_slot,
+                    (void*)d.tv_chunks, (void*)d.tv_pieces, (void*)d.tv_brow, (void*)d.tv_val,
+                    (void*)d.tv_mask,
                     (void*)d.tv_split, (void*)d.partials})
         if (p) (void)hipFree(p);
     if (d.device >= 0 && d.device != cur && cur >= 0) (void)hipSetDevice(cur);
@@ -268,7 +269,8 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.tv_n_chunks = (int32_t)(tv.chunks.size() / 4);
             d.tv_pieces = upload_array(tv.pieces, st, "upload tile pieces");
             d.tv_brow = upload_array(tv.brow, st, "upload tile entries");
-            d.tv_slot = upload_array(tv.slot, st, "upload tile slots");
+            d.tv_val = upload_array(tv.val, st, "upload tile values");
+            d.tv_mask = upload_array(tv.mask, st, "upload tile masks");
             d.tv_n_entries = tv.n_entries();
             d.tv_split = upload_array(tv.split, st, "upload split tiles");
             d.tv_n_split = (int32_t)(tv.split.size() / 4);

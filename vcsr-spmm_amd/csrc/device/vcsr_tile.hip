@@ -14,9 +14,10 @@
 // Work item (one wave): MERGE consecutive work items of the view, each a run
 // of tile pieces with at most tile_piece_entries(R) entries
 // (host/tile_view.hpp).
-// Phase 1 (lane per entry): read the entry's B row and R slot indices, gather
-// the R values from the VCSR value array and stage (B-row byte offset,
-// presence bits, values) in the wave's LDS list.
+// Phase 1 (lane per entry): read the entry's B row, presence bits and R
+// values (the view stores the values of its slots next to each other, so
+// these are coalesced loads, not gathers from the VCSR value array) and stage
+// (B-row byte offset, presence bits, values) in the wave's LDS list.
 // Phase 2, per column tile of LPE*VEC columns: the wave is S = 64/LPE
 // streams of LPE lanes; one load instruction serves one entry of every
 // stream.
@@ -46,26 +47,6 @@ constexpr int kWaves = 4;
 // Buffer offset of "no B row": at least 2^31, above any buffer-path B size,
 // and still below 2^32 after adding a column offset (< 2^31).
 constexpr uint32_t kNoRow = 0x80000000u;
-
-template <int R>
-__device__ __forceinline__ void load_slots(const int32_t* __restrict__ p, int32_t (&s)[R]) {
-    if constexpr (R == 1) {
-        s[0] = p[0];
-    } else if constexpr (R == 2) {
-        const int2 x = *reinterpret_cast<const int2*>(p);
-        s[0] = x.x;
-        s[1] = x.y;
-    } else {
-#pragma unroll
-        for (int q = 0; q < R; q += 4) {
-            const int4 x = *reinterpret_cast<const int4*>(p + q);
-            s[q] = x.x;
-            s[q + 1] = x.y;
-            s[q + 2] = x.z;
-            s[q + 3] = x.w;
-        }
-    }
-}
 
 template <int R>
 __device__ __forceinline__ void store_vals(float* p, const float (&a)[R]) {
@@ -120,8 +101,8 @@ __attribute__((amdgpu_waves_per_eu((R <= 3 && MERGE == 1) ? 5 : 1, 8)))
 void vcsr_tile_kernel(
     int32_t n_chunks, int32_t O, int32_t accumulate, uint32_t b_bytes,
     const int4* __restrict__ chunks, const int4* __restrict__ pieces,
-    const int32_t* __restrict__ ent_brow, const int32_t* __restrict__ ent_slot,
-    const float* __restrict__ val, const float* __restrict__ B, float* __restrict__ C,
+    const int32_t* __restrict__ ent_brow, const uint8_t* __restrict__ ent_mask,
+    const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
     float* __restrict__ partials) {
     using V = typename VecT<VEC>::T;
     constexpr int S = 64 / LPE;                              // streams per wave
@@ -156,19 +137,10 @@ void vcsr_tile_kernel(
     const uint32_t row_bytes = (uint32_t)O * 4u;
     for (int32_t i = lane; i < ne; i += 64) {
         const int64_t e = (int64_t)e0 + i;
-        int32_t sl[RS];
-        load_slots<RS>(ent_slot + e * RS, sl);
         const uint32_t br = (uint32_t)ent_brow[e];
+        const uint32_t m = ent_mask[e];
         float a[RS];
-        uint32_t m = 0;
-#pragma unroll
-        for (int r = 0; r < RS; ++r) {
-            a[r] = 0.f;
-            if (r < R && sl[r] >= 0) {  // slots past R are always -1
-                a[r] = val[sl[r]];
-                m |= 1u << r;
-            }
-        }
+        load_vals<RS>(ent_val + e * RS, a);
         lb[i] = BUF ? (m ? br * row_bytes : kNoRow) : br;
         lm[i] = (uint8_t)m;
         store_vals<RS>(lv + i * RS, a);
@@ -188,10 +160,13 @@ void vcsr_tile_kernel(
     const int sub = lane / LPE, kl = lane % LPE;
 
     // One entry's B slice; zeros for "no row" (placeholders, lanes past the
-    // end) on the buffer path.
+    // end) on the buffer path.  The offset is read for every lane (tc is a
+    // valid index) and lanes past the end get the "no row" bit ORed in, so
+    // the tail blocks issue their loads back to back like the full ones (a
+    // conditional read becomes a branch and an LDS wait per load).
     auto load_b = [&](int32_t tc, bool ok, uint32_t koff) -> V {
         if constexpr (BUF) {
-            const uint32_t off = ok ? lb[tc] + koff : kNoRow;
+            const uint32_t off = (lb[tc] + koff) | (ok ? 0u : kNoRow);
             return load_b_buf<VEC>(rsrc, off);
         } else {
             const V b = *reinterpret_cast<const V*>(B + (int64_t)lb[tc] * O + koff / 4);
@@ -441,7 +416,7 @@ hipError_t launch_one(const DeviceFmt& d, const float* B, int32_t O, float* C,
     const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves)), block(64 * kWaves);
     hipLaunchKernelGGL((vcsr_tile_kernel<VEC, LPE, R, MERGE, BUF>), grid, block, 0, st, d.tv_n_chunks, O,
                        accumulate, b_bytes, reinterpret_cast<const int4*>(d.tv_chunks),
-                       reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_slot, d.val, B,
+                       reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask, d.tv_val, B,
                        C, d.partials);
     return hipGetLastError();
 }

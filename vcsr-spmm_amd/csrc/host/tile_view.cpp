@@ -1,8 +1,8 @@
 // tile_view.cpp - builds the row-tile view of a VCSR format (tile_view.hpp).
 //
 // Everything is recovered from the packed VCSR arrays (group_ptr,
-// group_depth, group_seg_base, group_rows, lcol); the view holds indices
-// into them, never copies of the values.
+// group_depth, group_seg_base, group_rows, lcol, val): the view's slot
+// indices point into them and its values are copies of val[slot].
 #include "tile_view.hpp"
 
 #include <algorithm>
@@ -187,6 +187,8 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
     tv.brow.resize((size_t)E);
     const size_t stride = (size_t)tile_slot_stride(R);
     tv.slot.assign((size_t)E * stride, -1);
+    tv.val.assign((size_t)E * stride, 0.f);
+    tv.mask.assign((size_t)E, 0);
     parallel_for((int64_t)tiles.size(), 1024, nthreads, [&](int64_t tb, int64_t te) {
         std::vector<int32_t> u, w;
         for (int64_t t = tb; t < te; ++t) {
@@ -208,7 +210,10 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
                 const int64_t pe = rl.ptr[(size_t)(x.row0 + r) + 1];
                 for (size_t q = 0; q < u.size() && p < pe; ++q) {
                     if (rl.col[(size_t)p] == u[q]) {
-                        tv.slot[((size_t)e0 + q) * stride + (size_t)r] = rl.slot[(size_t)p];
+                        const size_t k = ((size_t)e0 + q) * stride + (size_t)r;
+                        tv.slot[k] = rl.slot[(size_t)p];
+                        tv.val[k] = v.val[(size_t)rl.slot[(size_t)p]];
+                        tv.mask[(size_t)e0 + q] |= (uint8_t)(1u << r);
                         ++p;
                     }
                 }
