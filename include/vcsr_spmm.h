@@ -137,9 +137,10 @@ int vcsr_fmt_arrays(const vcsr_fmt* fmt, vcsr_arrays* out);
  * src/vcsr_seg.cu:196-211.  The handle owns the device copy: no globals. */
 int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream);
 /* Tile height of the row-tile view vcsr_fmt_upload derives for the
- * tile-stationary kernel (VCSR_KERNEL_TILE): rows = 1, 2, 3, 4 or 8 forces it,
- * 0 (the default) picks it from the matrix.  Only before the upload
- * (VCSR_ESTATE after).  No reference counterpart. */
+ * tile-stationary kernel (VCSR_KERNEL_TILE): rows = 1, 2, 3, 4, 8 or 16
+ * forces it, 0 (the default) picks it from the matrix.  16-row tiles run on
+ * the FP32 matrix cores (dense sub-blocks, layout TC matrices).  Only before
+ * the upload (VCSR_ESTATE after).  No reference counterpart. */
 int vcsr_fmt_set_tile_rows(vcsr_fmt* fmt, int32_t rows);
 /* The uploaded view's tile height, tile count and entry count (B-row slice
  * loads per column tile of one SpMM; nnz for tile height 1).  No reference
@@ -218,6 +219,11 @@ int spmm_vcsr_mfma(const vcsr_fmt* fmt, const float* dB, int32_t O,
  * Host only (no upload needed).  No reference counterpart. */
 int vcsr_mfma_work(const vcsr_fmt* fmt, int32_t O, int32_t tileK, int64_t* ops,
                    int32_t* flops_per_op);
+/* The same for the tile-stationary kernel on an uploaded format whose view
+ * has 16-row tiles (v_mfma_f32_16x16x4f32 per four entries, column tile and
+ * column part, padding entries included); ops = 0 for other tile heights.
+ * No reference counterpart. */
+int vcsr_tile_mfma_work(const vcsr_fmt* fmt, int32_t O, int64_t* ops, int32_t* flops_per_op);
 
 /* CPU CSR SpMM, C = A*B in FP32, for each row: p ascending, k inner, one
  * fused multiply-add per term (the loop order of src/kernels.cu:25-32).

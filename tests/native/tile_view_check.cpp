@@ -50,6 +50,12 @@ static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, in
         if (e1 - e0 < 1 || e1 - e0 > cap) return fail("item entry count", M, R);
         if (p1 - p0 < 1 || p1 - p0 > kTileChunkPieces) return fail("item piece count", M, R);
         if (tv.pieces[4 * p0 + 2] != e0) return fail("item's first piece", M, R);
+        if (R == kTileMmaRows) {
+            // Matrix-core tiles: one piece per item, whole 16-entry groups.
+            if (p1 - p0 != 1) return fail("16-row item with several pieces", M, R);
+            if (e0 % kTileMmaGroup != 0 || (e1 - e0) % kTileMmaGroup != 0)
+                return fail("16-row item not in whole entry groups", M, R);
+        }
         for (int p = p0; p < p1; ++p) {
             const int pe = p + 1 < p1 ? tv.pieces[4 * (p + 1) + 2] : e1;
             if (pe - tv.pieces[4 * p + 2] < 1) return fail("empty piece", M, R);
@@ -68,13 +74,19 @@ static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, in
     for (int p = 0; p < np; ++p) {
         const int row0 = tv.pieces[4 * p], nr = tv.pieces[4 * p + 1], b = tv.pieces[4 * p + 2];
         const int e = p + 1 < np ? tv.pieces[4 * (p + 1) + 2] : (int)E;
+        int last = -1;  // B row of the piece's previous entry with a value
         for (int q = b; q < e; ++q) {
-            if (q > b && tv.brow[q] < tv.brow[q - 1]) return fail("entries not in column order", M, R);
+            if (tv.mask[q] == 0) {
+                if (tv.brow[q] != 0) return fail("placeholder entry reads a B row", M, R);
+            } else {
+                if (tv.brow[q] < last) return fail("entries not in column order", M, R);
+                last = tv.brow[q];
+            }
             for (int r = 0; r < RS; ++r) {
                 // The kernel reads the values and presence bits; the slots
                 // say where those values come from.
                 const int s = tv.slot[(size_t)q * RS + r];
-                const float a = tv.val[(size_t)q * RS + r];
+                const float a = tv.val[(size_t)tile_val_index(R, q, r)];
                 const bool present = (tv.mask[q] >> r) & 1;
                 if (present != (s >= 0)) return fail("presence bit differs from slot", M, R);
                 if (s < 0) {
@@ -160,8 +172,18 @@ int main() {
             const Csr a = block_matrix(10 + R, 30, 3, 300, 7, 3, 75, true);
             bad |= check(a, 4, 64, layout, R, R);
         }
+    // 16-row blocks: the automatic height is the matrix-core tile; 8-row
+    // blocks stay at 8 (two neighbouring blocks share no columns).
+    bad |= check(block_matrix(5, 12, 16, 900, 9, 16, 100, false), 4, 64, kLayoutS, 0, 16);
+    bad |= check(block_matrix(6, 12, 16, 900, 9, 16, 100, false), 16, 16, kLayoutTC, 0, 16);
+    for (int layout : {kLayoutH, kLayoutS, kLayoutTC}) {
+        bad |= check(block_matrix(7, 10, 16, 500, 7, 16, 75, true), 4, 64, layout, 16, 16);
+        bad |= check(block_matrix(8, 30, 3, 300, 7, 3, 75, true), 4, 64, layout, 16, 16);
+    }
+    bad |= check(cfg1, 4, 64, kLayoutS, 16, 16);
     // Tiles wider than one work item (split into pieces with partial sums).
     for (int R : {1, 3, 8}) bad |= check(block_matrix(20 + R, 6, 8, 4096, 300, 4, 90, false), 4, 64, kLayoutS, R, R);
+    bad |= check(block_matrix(36, 4, 16, 8192, 700, 4, 90, false), 4, 64, kLayoutS, 16, 16);
     // Empty rows and an empty matrix.
     {
         Coo c;
@@ -170,7 +192,7 @@ int main() {
         c.rows = {2, 2, 6};
         c.cols = {0, 4, 4};
         c.vals = {1.f, 2.f, 3.f};
-        for (int R : {0, 1, 2, 4}) bad |= check(coo_to_csr(c), 4, 64, kLayoutS, R, R ? R : 0);
+        for (int R : {0, 1, 2, 4, 16}) bad |= check(coo_to_csr(c), 4, 64, kLayoutS, R, R ? R : 0);
         Coo z;
         z.M = 7;
         z.N = 3;

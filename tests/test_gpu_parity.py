@@ -300,7 +300,8 @@ def _block_csr(vs, rng, nbr, bh, N, blocks_per_row, bw, keep):
 
 
 @pytest.mark.parametrize("bh,tile_rows", [(2, 0), (3, 0), (4, 0), (8, 0), (16, 0), (3, 1), (3, 2),
-                                          (3, 3), (6, 3), (3, 8), (5, 4)])
+                                          (3, 3), (6, 3), (3, 8), (5, 4), (16, 16), (5, 16),
+                                          (12, 16)])
 @pytest.mark.parametrize("O", [1, 8, 33, 128, 200, 520])
 def test_tile_kernel_block_rows(gpu, orc, st, bh, tile_rows, O):
     vs = gpu
@@ -325,7 +326,7 @@ def test_tile_kernel_block_rows(gpu, orc, st, bh, tile_rows, O):
         assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"bh{bh} R{R} O{O}")
 
 
-@pytest.mark.parametrize("tile_rows", [1, 3, 4, 8])
+@pytest.mark.parametrize("tile_rows", [1, 3, 4, 8, 16])
 def test_tile_kernel_split_tiles(gpu, orc, st, tile_rows):
     """Block rows wider than one work item: tiles are cut into pieces whose
     partial sums a second kernel adds; wider O grows the scratch."""
@@ -342,8 +343,9 @@ def test_tile_kernel_split_tiles(gpu, orc, st, tile_rows):
         assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"R{tile_rows} O{O}")
 
 
-@pytest.mark.parametrize("kind", ["csr", "segment", "row", "tile"])
-def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind):
+@pytest.mark.parametrize("kind,tile_rows", [("csr", 4), ("segment", 4), ("row", 4), ("tile", 4),
+                                            ("tile", 16)])
+def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind, tile_rows):
     """Inf and NaN in B reach exactly the C entries whose rows have a nonzero
     in that B row (an absent entry contributes nothing, not 0 * inf).  The
     MFMA kernel is left out: it multiplies every group as a dense tile, so a
@@ -358,7 +360,7 @@ def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind):
     B[17, :] = np.nan
     B[40, 7] = -np.inf
     ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
-    C = _run(vs, kind, csr, B, st, tile_rows=4)
+    C = _run(vs, kind, csr, B, st, tile_rows=tile_rows)
     assert np.array_equal(np.isnan(C), np.isnan(ref)), kind
     assert np.array_equal(np.isposinf(C), np.isposinf(ref)), kind
     assert np.array_equal(np.isneginf(C), np.isneginf(ref)), kind
@@ -366,8 +368,8 @@ def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind):
     assert np.allclose(C[fin], ref[fin], rtol=1e-5, atol=1e-4)
 
 
-@pytest.mark.parametrize("kind", ["row", "tile"])
-def test_b_of_2gb_or_more_uses_64bit_addresses(gpu, orc, st, kind):
+@pytest.mark.parametrize("kind,tile_rows", [("row", 0), ("tile", 0), ("tile", 16)])
+def test_b_of_2gb_or_more_uses_64bit_addresses(gpu, orc, st, kind, tile_rows):
     """B of 2^31 bytes or more cannot be addressed with 32-bit buffer
     offsets; the row and tile kernels then take their 64-bit-address path.
     N = 2^19 + 3 rows of O = 1024 floats (2.0 GiB + 12 KiB), 3000 sparse rows
@@ -383,5 +385,32 @@ def test_b_of_2gb_or_more_uses_64bit_addresses(gpu, orc, st, kind):
     csr = vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
     B = vs.gen_dense(77, 0, N, O)
     assert B.nbytes >= 1 << 31
-    C = _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=128)
+    C = _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=128, tile_rows=tile_rows)
     _rowsample_check(vs, orc, csr, B, C, 300, 21)
+
+
+@pytest.mark.parametrize("O", [8, 32, 100, 512])
+def test_tile_mfma_work_counts_the_launch(gpu, orc, st, O):
+    """The MFMA instruction count of 16-row tiles: four entries per k-step,
+    16*VEC columns per column tile, one MFMA per column part (VEC = 4, 2 or 1
+    by O); none for other tile heights.  The result is checked too."""
+    vs = gpu
+    rng = np.random.default_rng(O)
+    csr = _block_csr(vs, rng, 9, 16, 400, 6, 16, 1.0)
+    B = vs.gen_dense(O, 0, csr.N, O)
+    fmt = vs.build_vcsr(csr, 16, 16, vs.LAYOUT_TC)
+    fmt.upload(st)
+    R, tiles, entries = fmt.tile_info()
+    assert (R, tiles) == (16, 9)
+    assert entries % 16 == 0 and entries >= csr.nnz // 16
+    vec = 4 if O % 4 == 0 and O >= 64 else (2 if O % 2 == 0 and O >= 32 else 1)
+    ops, fpo = vs.tile_mfma_work(fmt, O)
+    assert fpo == 2 * 16 * 16 * 4
+    assert ops == entries // 4 * -(-O // (16 * vec)) * vec
+    got = _ex(vs, fmt, B, np.zeros((csr.M, O), np.float32), st, vs.KERNEL_TILE, False)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"O{O}")
+    other = vs.build_vcsr(csr, 16, 16, vs.LAYOUT_TC)
+    other.set_tile_rows(8)
+    other.upload(st)
+    assert vs.tile_mfma_work(other, O)[0] == 0

@@ -42,7 +42,7 @@ EXPORTS = (
     "vcsr_coo_free vcsr_gen_coo vcsr_gen_dense vcsr_coo_to_csr vcsr_csr_create "
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
     "vcsr_fmt_set_tile_rows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_vcsr "
-    "spmm_vcsr_ex spmm_vcsr_mfma vcsr_mfma_work spmm_csr_cpu "
+    "spmm_vcsr_ex spmm_vcsr_mfma vcsr_mfma_work vcsr_tile_mfma_work spmm_csr_cpu "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
     "vcsr_memcpy_d2h vcsr_memcpy_d2d vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
     "vcsr_stream_sync vcsr_device_sync vcsr_event_create vcsr_event_destroy "
@@ -115,6 +115,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "spmm_vcsr_ex": (C.c_int, [P, P, I32, I32, P, P, pF, I32, I32]),
         "spmm_vcsr_mfma": (C.c_int, [P, P, I32, P, P, pF]),
         "vcsr_mfma_work": (C.c_int, [P, I32, I32, C.POINTER(I64), pI]),
+        "vcsr_tile_mfma_work": (C.c_int, [P, I32, C.POINTER(I64), pI]),
         "spmm_csr_cpu": (C.c_int, [I32, P, P, P, P, I32, P, I32]),
         "vcsr_device_count": (C.c_int, [pI]),
         "vcsr_device_name": (C.c_int, [C.c_char_p, I32]),
@@ -436,6 +437,15 @@ def mfma_work(fmt: Vcsr, O: int, tileK: int = 0) -> tuple[int, int]:
     for one SpMM of width O (host only)."""
     ops, fpo = C.c_int64(), C.c_int32()
     _check(load_library().vcsr_mfma_work(fmt._h, O, tileK, C.byref(ops), C.byref(fpo)))
+    return ops.value, fpo.value
+
+
+def tile_mfma_work(fmt: Vcsr, O: int) -> tuple[int, int]:
+    """(MFMA instructions, FLOPs per instruction) the tile-stationary kernel
+    issues for one SpMM of width O on an uploaded format with 16-row tiles
+    ((0, flops) for other tile heights)."""
+    ops, fpo = C.c_int64(), C.c_int32()
+    _check(load_library().vcsr_tile_mfma_work(fmt._h, O, C.byref(ops), C.byref(fpo)))
     return ops.value, fpo.value
 
 

@@ -211,8 +211,9 @@ int vcsr_fmt_arrays(const vcsr_fmt* fmt, vcsr_arrays* out) {
 int vcsr_fmt_set_tile_rows(vcsr_fmt* fmt, int32_t rows) {
     return guarded([&] {
         need(fmt != nullptr, "null format");
-        need(rows == 0 || rows == 1 || rows == 2 || rows == 3 || rows == 4 || rows == 8,
-             "tile rows must be 0, 1, 2, 3, 4 or 8");
+        need(rows == 0 || rows == 1 || rows == 2 || rows == 3 || rows == 4 || rows == 8 ||
+                 rows == 16,
+             "tile rows must be 0, 1, 2, 3, 4, 8 or 16");
         if (fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format already uploaded");
         fmt->tile_rows = rows;
     });

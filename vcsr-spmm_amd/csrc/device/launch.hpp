@@ -46,6 +46,10 @@ hipError_t launch_vcsr_rowmajor(const Vcsr& v, const DeviceFmt& d, const float* 
 // Needs d.partials sized for O when the view has split tiles.
 hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                             float* C, int32_t accumulate, hipStream_t st);
+// MFMA instructions launch_vcsr_tile issues for one SpMM of width O when
+// the view has 16-row tiles (none otherwise), as launched for the alignment
+// of 16-byte aligned B and C.
+MfmaWork tile_mfma_work(const DeviceFmt& d, int32_t O);
 
 // A row-stationary work item covers at most this many (group, lane) pair
 // records (one per lane) and entries (the wave's LDS list); longer rows are

@@ -365,6 +365,17 @@ int vcsr_mfma_work(const vcsr_fmt* fmt, int32_t O, int32_t tileK, int64_t* ops,
     });
 }
 
+int vcsr_tile_mfma_work(const vcsr_fmt* fmt, int32_t O, int64_t* ops, int32_t* flops_per_op) {
+    return guarded([&] {
+        need(fmt && ops && flops_per_op, "null argument");
+        need(O >= 0, "negative O");
+        if (!fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format not uploaded");
+        const vcsr::MfmaWork w = vcsr::tile_mfma_work(fmt->dev, O);
+        *ops = w.ops;
+        *flops_per_op = w.flops_per_op;
+    });
+}
+
 int vcsr_device_count(int32_t* n) {
     return guarded([&] {
         need(n != nullptr, "null output");

@@ -101,7 +101,7 @@ __attribute__((amdgpu_waves_per_eu((R <= 3 && MERGE == 1) ? 5 : 1, 8)))
 void vcsr_tile_kernel(
     int32_t n_chunks, int32_t O, int32_t accumulate, uint32_t b_bytes,
     const int4* __restrict__ chunks, const int4* __restrict__ pieces,
-    const int32_t* __restrict__ ent_brow, const uint8_t* __restrict__ ent_mask,
+    const int32_t* __restrict__ ent_brow, const uint16_t* __restrict__ ent_mask,
     const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
     float* __restrict__ partials) {
     using V = typename VecT<VEC>::T;
@@ -404,6 +404,179 @@ __global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t O, int32_t accum
     }
 }
 
+// ---------------------------------------------------------------------------
+// 16-row tiles on the matrix cores (view height kTileMmaRows).
+//
+// v_mfma_f32_16x16x4f32 computes D[i][j] += sum_k A[i][k] * B[k][j] for a
+// 16 x 4 A and a 4 x 16 B, with A[i][k] in lane 16k + i, B[k][j] in lane
+// 16k + j and D[4q + v][j] in register v of lane 16q + j (checked on the
+// device).  Here A is the tile's values for four entries (k) and its 16 rows
+// (i), and B the four entries' B-row slices: lane 16k + j holds VEC columns
+// c0 + VEC*j .. + VEC-1 of entry k's B row, and MFMA number c takes
+// component c, so D_c[i][j] is C[row i][c0 + VEC*j + c].  A group of 16
+// entries is four k-steps; the view stores its values in operand order, so
+// lane l reads the A operands of all four as one 16-byte load.
+//
+// One wave per (piece, column tile of 16*VEC columns).  The grid runs
+// column-tile-major with the XCD-aware block order, so each XCD works on one
+// column range of B at a time and its L2 holds that slice of B (the B rows a
+// block-sparse matrix touches are spread over all of B).
+// ---------------------------------------------------------------------------
+typedef float mma_acc4 __attribute__((ext_vector_type(4)));
+constexpr int kMmaWaves = 4;
+constexpr int kMmaPiece = tile_piece_entries(kTileMmaRows);
+
+template <int VEC>
+__device__ __forceinline__ float vec_part(const typename VecT<VEC>::T& b, int c) {
+    return reinterpret_cast<const float*>(&b)[c];
+}
+
+template <int VEC, bool BUF>
+__global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
+    int32_t n_items, int32_t n_ctiles, int32_t O, int32_t accumulate, uint32_t b_bytes,
+    const int4* __restrict__ chunks, const int4* __restrict__ pieces,
+    const int32_t* __restrict__ ent_brow, const uint16_t* __restrict__ ent_mask,
+    const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
+    float* __restrict__ partials) {
+    using V = typename VecT<VEC>::T;
+    constexpr int GU = 2;  // entry groups (of 16) per block of loads
+    __shared__ uint32_t s_brow[kMmaWaves][kMmaPiece];
+
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63);
+    const int64_t w = (int64_t)xcd_remap(blockIdx.x, gridDim.x) * kMmaWaves + wave;
+    if (w >= (int64_t)n_items * n_ctiles) return;
+    const int32_t ct = (int32_t)(w / n_items), item = (int32_t)(w - (int64_t)ct * n_items);
+    const int32_t e0 = uniform(chunks[item].x), ne = uniform(chunks[item].y) - e0;  // 16 | ne
+    const int32_t pidx = uniform(chunks[item].z);
+    const int32_t row0 = uniform(pieces[pidx].x), rows = uniform(pieces[pidx].y);
+    const int32_t part = uniform(pieces[pidx].w);
+    uint32_t* lb = s_brow[wave];
+
+    // Phase 1: B-row byte offsets (row indices without the buffer path) of
+    // the piece's entries; placeholders get "no row".
+    const uint32_t row_bytes = (uint32_t)O * 4u;
+    for (int32_t i = lane; i < ne; i += 64) {
+        const uint32_t br = (uint32_t)ent_brow[e0 + i];
+        const bool any = ent_mask[e0 + i] != 0;
+        lb[i] = BUF ? (any ? br * row_bytes : kNoRow) : (any ? br : kNoRow);
+    }
+    wave_sync();
+
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), (short)0, (int)b_bytes,
+                                          kRawBufferFlags);
+    const int kq = lane >> 4, jl = lane & 15;  // MFMA k index, column lane
+    const int32_t col = ct * 16 * VEC + VEC * jl;
+    const bool kok = col < O;
+    const uint32_t koff = (uint32_t)(kok ? col : 0) * 4u;
+    // Entry t's B slice for this lane; zeros for "no row" and columns past O.
+    auto load_b = [&](int32_t t) -> V {
+        if constexpr (BUF) {
+            return load_b_buf<VEC>(rsrc, (lb[t] + koff) | (kok ? 0u : kNoRow));
+        } else {
+            const uint32_t br = lb[t];
+            if (br == kNoRow || !kok) return zero_vec(V());
+            return *reinterpret_cast<const V*>(B + (int64_t)br * O + col);
+        }
+    };
+    const float* vp = ent_val + (int64_t)e0 * kTileMmaRows + 4 * lane;
+
+    mma_acc4 d[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) d[c] = mma_acc4{0.f, 0.f, 0.f, 0.f};
+    auto block = [&](auto n_c, int32_t g0) {
+        constexpr int NG = decltype(n_c)::value;
+        float4 a[NG];
+        V b[NG][4];
+#pragma unroll
+        for (int gu = 0; gu < NG; ++gu) {
+            a[gu] = *reinterpret_cast<const float4*>(vp + (int64_t)(g0 + gu) * 256);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) b[gu][s] = load_b(16 * (g0 + gu) + 4 * s + kq);
+        }
+#pragma unroll
+        for (int gu = 0; gu < NG; ++gu)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int c = 0; c < VEC; ++c)
+                    d[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        reinterpret_cast<const float*>(&a[gu])[s], vec_part<VEC>(b[gu][s], c), d[c],
+                        0, 0, 0);
+    };
+    const int32_t ng = ne / kTileMmaGroup;
+    int32_t g0 = 0;
+    for (; g0 + GU <= ng; g0 += GU) block(std::integral_constant<int, GU>(), g0);
+    if (g0 < ng) block(std::integral_constant<int, 1>(), g0);
+
+    // This lane holds rows 4*kq + v of the tile, columns col .. col+VEC-1.
+    bool fin = true;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int c = 0; c < VEC; ++c)
+            if (4 * kq + v < rows) fin = fin && __builtin_isfinite(d[c][v]);
+    if (__any(!(fin || !kok))) {
+        // A non-finite sum: recompute this lane's rows in entry order on the
+        // VALU, skipping the rows an entry does not have (0 * inf must not
+        // reach them), like the reference's per-row loop.
+        V acc[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] = zero_vec(V());
+        for (int32_t t = 0; t < ne; ++t) {
+            const uint32_t m = ent_mask[e0 + t];
+            const V b = load_b(t);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = 4 * kq + v;
+                if ((m >> r) & 1u)
+                    fma_vec(acc[v], ent_val[tile_val_index(kTileMmaRows, (int64_t)e0 + t, r)], b);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int c = 0; c < VEC; ++c) d[c][v] = reinterpret_cast<const float*>(&acc[v])[c];
+    }
+    if (!kok) return;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int r = 4 * kq + v;
+        if (r >= rows) continue;
+        V x;
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) reinterpret_cast<float*>(&x)[c] = d[c][v];
+        if (part < 0) {
+            V* dst = reinterpret_cast<V*>(C + (int64_t)(row0 + r) * O + col);
+            store_nt(dst, accumulate ? add_vec(*dst, x) : x);
+        } else {
+            *reinterpret_cast<V*>(partials + (int64_t)(part + r) * O + col) = x;
+        }
+    }
+}
+
+template <int VEC>
+hipError_t launch_mma(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, float* C,
+                      int32_t accumulate, hipStream_t st) {
+    const int32_t n_ct = (O + 16 * VEC - 1) / (16 * VEC);
+    const int64_t waves = (int64_t)d.tv_n_chunks * n_ct;
+    const dim3 grid((unsigned)((waves + kMmaWaves - 1) / kMmaWaves)), block(64 * kMmaWaves);
+    const uint64_t b_bytes = (uint64_t)v.N * (uint64_t)O * 4u;
+    if (b_bytes + 64u * 4u * (uint64_t)VEC >= kBufferLimit)
+        hipLaunchKernelGGL((vcsr_tile_mma_kernel<VEC, false>), grid, block, 0, st, d.tv_n_chunks,
+                           n_ct, O, accumulate, 0u, reinterpret_cast<const int4*>(d.tv_chunks),
+                           reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask,
+                           d.tv_val, B, C, d.partials);
+    else
+        hipLaunchKernelGGL((vcsr_tile_mma_kernel<VEC, true>), grid, block, 0, st, d.tv_n_chunks,
+                           n_ct, O, accumulate, (uint32_t)b_bytes,
+                           reinterpret_cast<const int4*>(d.tv_chunks),
+                           reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask,
+                           d.tv_val, B, C, d.partials);
+    return hipGetLastError();
+}
+
 template <int VEC, int LPE, int R, bool BUF>
 hipError_t launch_one(const DeviceFmt& d, const float* B, int32_t O, float* C,
                       int32_t accumulate, uint32_t b_bytes, hipStream_t st) {
@@ -452,6 +625,7 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
             case 3: e = launch_r<VEC, 3>(d, B, O, C, accumulate, b_bytes, st); break;
             case 4: e = launch_r<VEC, 4>(d, B, O, C, accumulate, b_bytes, st); break;
             case 8: e = launch_r<VEC, 8>(d, B, O, C, accumulate, b_bytes, st); break;
+            case kTileMmaRows: e = launch_mma<VEC>(v, d, B, O, C, accumulate, st); break;
             default: return hipErrorInvalidValue;
         }
         if (e != hipSuccess) return e;
@@ -467,6 +641,14 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
 
 }  // namespace
 
+// Floats per lane and B slice: 4 when O allows 16 lanes of 16-byte vectors
+// and B and C are 16-byte aligned, else 2 or 1.
+static int tile_vec(int32_t O, bool a16, bool a8) {
+    if (O % 4 == 0 && a16 && O >= 64) return 4;
+    if (O % 2 == 0 && a8 && O >= 32) return 2;
+    return 1;
+}
+
 hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                             float* C, int32_t accumulate, hipStream_t st) {
     if (O <= 0 || v.M == 0) return hipSuccess;
@@ -475,9 +657,21 @@ hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, i
     // Narrow B: narrower per-lane vectors give streams of at least 8-16
     // lanes, so fewer streams share a tile's entries (measured at O = 8:
     // 4-byte loads with 8 streams 1.3x faster than 16-byte loads with 32).
-    if (O % 4 == 0 && a16 && O >= 64) return launch_vec<4>(v, d, B, O, C, accumulate, st);
-    if (O % 2 == 0 && a8 && O >= 32) return launch_vec<2>(v, d, B, O, C, accumulate, st);
-    return launch_vec<1>(v, d, B, O, C, accumulate, st);
+    switch (tile_vec(O, a16, a8)) {
+        case 4: return launch_vec<4>(v, d, B, O, C, accumulate, st);
+        case 2: return launch_vec<2>(v, d, B, O, C, accumulate, st);
+        default: return launch_vec<1>(v, d, B, O, C, accumulate, st);
+    }
+}
+
+MfmaWork tile_mfma_work(const DeviceFmt& d, int32_t O) {
+    MfmaWork w;
+    w.flops_per_op = 2 * 16 * 16 * 4;
+    if (d.tv_R != kTileMmaRows || O <= 0) return w;
+    const int vec = tile_vec(O, true, true);
+    const int64_t n_ct = (O + 16 * vec - 1) / (16 * vec);
+    w.ops = d.tv_n_entries / 4 * n_ct * vec;
+    return w;
 }
 
 }  // namespace vcsr

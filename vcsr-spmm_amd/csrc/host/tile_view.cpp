@@ -149,22 +149,30 @@ std::vector<Tile> make_tiles(const RowLists& rl, int32_t M, int32_t cap, int nth
 }  // namespace
 
 TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
-    if (R != 0 && R != 1 && R != 2 && R != 3 && R != 4 && R != 8)
-        throw Error(kEinval, "tile height must be 0, 1, 2, 3, 4 or 8");
+    if (R != 0 && R != 1 && R != 2 && R != 3 && R != 4 && R != 8 && R != kTileMmaRows)
+        throw Error(kEinval, "tile height must be 0, 1, 2, 3, 4, 8 or 16");
     if (nthreads <= 0) nthreads = default_threads();
     const int32_t M = v.M;
     const RowLists rl = row_lists(v, nthreads);
 
     // Tile height: modelled cost per union entry = one B-row slice load
-    // (about 16 cycles of the vector memory pipe) + R accumulator updates.
+    // (about 20 cycles of the vector memory pipe) + R accumulator updates on
+    // the VALU; 16-row tiles run on the matrix cores, where an entry costs
+    // about 4 such updates, but only pay off when the tiles are tall (16-row
+    // MFMA operands are wasted on short tiles), so they are considered only
+    // when their mean height is at least 12 rows.
     std::vector<Tile> tiles;
+    auto pad = [](int32_t cap, int64_t n) {
+        return cap == kTileMmaRows ? (n + kTileMmaGroup - 1) / kTileMmaGroup * kTileMmaGroup : n;
+    };
     if (R == 0) {
         double best = 0;
-        for (int32_t cap : {1, 2, 3, 4, 8}) {
+        for (int32_t cap : {1, 2, 3, 4, 8, kTileMmaRows}) {
             std::vector<Tile> t = make_tiles(rl, M, cap, nthreads);
             int64_t ent = 0;
-            for (const Tile& x : t) ent += x.nent;
-            const double cost = (double)ent * (16.0 + cap);
+            for (const Tile& x : t) ent += pad(cap, x.nent);
+            if (cap == kTileMmaRows && (int64_t)t.size() * 12 > (int64_t)M) continue;
+            const double cost = (double)ent * (16.0 + (cap == kTileMmaRows ? 4 : cap));
             if (R == 0 || cost < best) {
                 best = cost;
                 R = cap;
@@ -176,6 +184,8 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
     } else {
         tiles = make_tiles(rl, M, R, nthreads);
     }
+    if (R == kTileMmaRows)
+        for (Tile& x : tiles) x.nent = pad(R, x.nent);
 
     TileView tv;
     tv.R = R;
@@ -187,8 +197,9 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
     tv.brow.resize((size_t)E);
     const size_t stride = (size_t)tile_slot_stride(R);
     tv.slot.assign((size_t)E * stride, -1);
-    tv.val.assign((size_t)E * stride, 0.f);
     tv.mask.assign((size_t)E, 0);
+    const size_t nval = R == kTileMmaRows ? (size_t)E * kTileMmaRows : (size_t)E * stride;
+    tv.val.assign(nval, 0.f);
     parallel_for((int64_t)tiles.size(), 1024, nthreads, [&](int64_t tb, int64_t te) {
         std::vector<int32_t> u, w;
         for (int64_t t = tb; t < te; ++t) {
@@ -200,10 +211,10 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
                 u.swap(w);
             }
             const int64_t e0 = eoff[(size_t)t];
-            if (u.empty()) {
-                tv.brow[(size_t)e0] = 0;  // placeholder entry: every slot -1
-                continue;
-            }
+            // Placeholder entries (a tile of empty rows, the padding of a
+            // 16-row tile) read B row 0 with every slot -1.
+            for (int64_t q = 0; q < x.nent; ++q) tv.brow[(size_t)(e0 + q)] = 0;
+            if (u.empty()) continue;
             for (size_t q = 0; q < u.size(); ++q) tv.brow[(size_t)e0 + q] = u[q];
             for (int32_t r = 0; r < x.nrows; ++r) {
                 int64_t p = rl.ptr[(size_t)(x.row0 + r)];
@@ -212,8 +223,9 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
                     if (rl.col[(size_t)p] == u[q]) {
                         const size_t k = ((size_t)e0 + q) * stride + (size_t)r;
                         tv.slot[k] = rl.slot[(size_t)p];
-                        tv.val[k] = v.val[(size_t)rl.slot[(size_t)p]];
-                        tv.mask[(size_t)e0 + q] |= (uint8_t)(1u << r);
+                        tv.val[(size_t)tile_val_index(R, e0 + (int64_t)q, r)] =
+                            v.val[(size_t)rl.slot[(size_t)p]];
+                        tv.mask[(size_t)e0 + q] |= (uint16_t)(1u << r);
                         ++p;
                     }
                 }
@@ -237,16 +249,23 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
         cp0 = np;
     };
     int64_t n_partial = 0;
+    // 16-row tiles: every tile gets work items of its own, cut at multiples
+    // of kTileMmaGroup entries.
+    const int64_t align = R == kTileMmaRows ? kTileMmaGroup : 1;
     for (size_t t = 0; t < tiles.size(); ++t) {
         const Tile& x = tiles[t];
         const int64_t e0 = eoff[t];
-        if (x.nent > cap_e / 2) {
+        if (x.nent > cap_e / 2 || R == kTileMmaRows) {
             close_chunk(e0);
             const int64_t npc = (x.nent + cap_p - 1) / cap_p;
-            const int64_t size = (x.nent + npc - 1) / npc;
+            // Equal pieces in units of `align` entries (x.nent is a multiple).
+            const int64_t units = x.nent / align;
             const int64_t base = n_partial;
             for (int64_t j = 0; j < npc; ++j) {
-                const int64_t a = e0 + j * size, e = std::min(e0 + x.nent, a + size);
+                const int64_t a = align == 1 ? e0 + j * ((x.nent + npc - 1) / npc)
+                                             : e0 + align * (j * units / npc);
+                const int64_t e = align == 1 ? std::min(e0 + x.nent, a + (x.nent + npc - 1) / npc)
+                                             : e0 + align * ((j + 1) * units / npc);
                 const int32_t pi = (int32_t)(tv.pieces.size() / 4);
                 tv.pieces.insert(tv.pieces.end(),
                                  {x.row0, x.nrows, (int32_t)a,

@@ -29,15 +29,36 @@ namespace vcsr {
 // their B rows); for narrow B the kernel merges several consecutive items
 // per wave.
 constexpr int32_t tile_chunk_entries(int32_t R) { return 32 * R; }
+// Tile height of the matrix-core path: a tile of up to 16 rows is one MFMA
+// operand (v_mfma_f32_16x16x4f32: 16 rows x 4 entries of A against 4 B-row
+// slices).  Its entries come in groups of kTileMmaGroup (four MFMA k-steps;
+// a tile's entry count is padded up to a multiple), and every piece is a
+// work item of its own.
+constexpr int32_t kTileMmaRows = 16;
+constexpr int32_t kTileMmaGroup = 16;
 // Entries of one piece of a tile longer than half a work item (it gets work
 // items of its own): at least 64, so a long row is cut into fewer pieces
 // (and partial rows for the reduce kernel); larger pieces unbalance the
 // streams when several work items share a wave (narrow B).  The kernel's
 // LDS list holds this many entries per merged work item.
-constexpr int32_t tile_piece_entries(int32_t R) { return 32 * R > 64 ? 32 * R : 64; }
+constexpr int32_t tile_piece_entries(int32_t R) {
+    return R == kTileMmaRows ? 1024 : (32 * R > 64 ? 32 * R : 64);
+}
 // Slot indices stored per entry for tile height R (a power of two, so that
 // an entry's slots and staged values are one aligned vector).
-constexpr int32_t tile_slot_stride(int32_t R) { return R <= 2 ? R : (R <= 4 ? 4 : 8); }
+constexpr int32_t tile_slot_stride(int32_t R) {
+    return R <= 2 ? R : (R <= 4 ? 4 : (R <= 8 ? 8 : 16));
+}
+// Position of the value of entry e, tile row r in the view's value array.
+// Up to 8 rows: entry-major (e * stride + r).  16 rows: MFMA operand order,
+// so that lane l of a wave reads the A operands of four k-steps as one
+// 16-byte vector: within group g = e / 16 of 256 values, entry 16g + 4s + k
+// and row r sit at 4 * (16k + r) + s (k-step s, MFMA k-index k).
+constexpr int64_t tile_val_index(int32_t R, int64_t e, int32_t r) {
+    return R != kTileMmaRows
+               ? e * tile_slot_stride(R) + r
+               : (e / 16) * 256 + 4 * (16 * ((e % 16) % 4) + r) + (e % 16) / 4;
+}
 // Tile pieces per work item.
 constexpr int32_t kTileChunkPieces = 32;
 // Rows are cut into tiles inside fixed blocks of this many rows (so that
@@ -46,7 +67,7 @@ constexpr int32_t kTileChunkPieces = 32;
 constexpr int32_t kTileRowBlock = 4096;
 
 struct TileView {
-    int32_t R = 1;                // accumulator rows per tile: 1, 2, 3, 4 or 8
+    int32_t R = 1;                // accumulator rows per tile: 1, 2, 3, 4, 8 or 16
     int32_t n_tiles = 0;
     // Work items, 4 ints each: first entry, end entry, first piece, end piece.
     std::vector<int32_t> chunks;
@@ -56,10 +77,11 @@ struct TileView {
     std::vector<int32_t> brow;    // per entry: B row = segment base + local column
     // tile_slot_stride(R) per entry: VCSR slot for tile row r, or -1.
     std::vector<int32_t> slot;
-    // tile_slot_stride(R) per entry: the value of that slot (0 for -1).
+    // tile_slot_stride(R) per entry: the value of that slot (0 for -1), at
+    // tile_val_index(R, e, r).
     std::vector<float> val;
     // Per entry: bit r set where tile row r has the entry's column.
-    std::vector<uint8_t> mask;
+    std::vector<uint16_t> mask;
     // Rows of split tiles, 4 ints each: row, first partial row, stride
     // between the piece partials of that row, piece count.
     std::vector<int32_t> split;
@@ -68,7 +90,8 @@ struct TileView {
 };
 
 // Builds the view.  R = 0 picks the tile height that minimises the modelled
-// cost (B-row loads plus accumulator updates); R = 1, 2, 3, 4 or 8 forces it.
+// cost (B-row loads plus accumulator updates); R = 1, 2, 3, 4, 8 or 16 forces
+// it.
 TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads);
 
 }  // namespace vcsr
