@@ -253,17 +253,25 @@ def main():
                      "traffic": measured_traffic(args.config, args.algo),
                      "bytes_alg": bytes_alg},
     }
-    if args.algo == "mfma":
-        # Matrix-core utilisation: issued MFMA FLOPs (dense group tiles,
-        # padding included) per kernel time against the dense FP32 MFMA peak,
-        # and the useful share of the issued FLOPs.
-        ops, fpo = vs.mfma_work(fmt, O, tileK)
+    # The tile-stationary kernel runs 16-row tiles on the matrix cores.
+    tile_mma = args.algo in ("vcsr", "tile") and tr == 16
+    if args.algo == "mfma" or tile_mma:
+        # Matrix-core utilisation: issued MFMA FLOPs (dense group tiles or
+        # 16-row tiles, padding included) per kernel time against the dense
+        # FP32 MFMA peak, and the useful share of the issued FLOPs.  The
+        # roofline that binds is then the FP32 MFMA peak (useful FLOPs).
+        ops, fpo = vs.tile_mfma_work(fmt, O) if tile_mma else vs.mfma_work(fmt, O, tileK)
         issued = float(ops) * fpo
         rate = issued / (kernel_ms * 1e-3) / 1e12
         out["mfma"] = {"instructions": ops, "issued_gflop": round(issued / 1e9, 4),
                        "useful_frac": round(flop / issued, 4) if issued else None,
                        "tflops_issued": round(rate, 2), "peak_tflops": MFMA_FP32_PEAK_TFS,
                        "utilization": round(rate / MFMA_FP32_PEAK_TFS, 4)}
+        useful = flop / (kernel_ms * 1e-3) / 1e12
+        out["roofline"] = {"bound": "mfma", "achieved": round(useful, 2),
+                           "peak": MFMA_FP32_PEAK_TFS, "unit": "TFLOP/s",
+                           "frac": round(useful / MFMA_FP32_PEAK_TFS, 4),
+                           "traffic": out["roofline"]["traffic"], "bytes_alg": bytes_alg}
     if not args.no_cpu_baseline:
         gf, reps, secs = cpu_baseline(orc, csr, B, args.cpu_seconds)
         out["cpu_baseline"] = {"value": round(gf, 3), "unit": "GFLOP/s", "cores": 1,

@@ -290,13 +290,15 @@ int main(int argc, char** argv) {
         }
         report_check(label);
         report_roofline(sum / o.repeat);
-        if (mfma) {
-            // Utilisation of the matrix cores: useful FLOPs over issued MFMA
-            // FLOPs (padding of the dense group tiles), and the issued rate
-            // over the dense FP32 MFMA peak of MI355X (157.3 TFLOP/s).
-            int64_t ops = 0;
-            int32_t fpo = 0;
-            CHECK(vcsr_mfma_work(fmt, O, 0, &ops, &fpo));
+        // Utilisation of the matrix cores, for the MFMA kernel and for the
+        // default kernel when its view has 16-row (MFMA) tiles: useful FLOPs
+        // over issued MFMA FLOPs (padding of the dense tiles), and the issued
+        // rate over the dense FP32 MFMA peak of MI355X (157.3 TFLOP/s).
+        int64_t ops = 0;
+        int32_t fpo = 0;
+        if (mfma) CHECK(vcsr_mfma_work(fmt, O, 0, &ops, &fpo));
+        else CHECK(vcsr_tile_mfma_work(fmt, O, &ops, &fpo));
+        if (ops > 0) {
             const double issued = (double)ops * fpo;
             const double rate = issued / ((sum / o.repeat) * 1e-3) / 1e12;
             std::printf("mfma: %lld instructions, %.3f GFLOP issued, useful %.1f%%, "

@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
     const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
     float* __restrict__ partials) {
     using V = typename VecT<VEC>::T;
-    constexpr int GU = 2;  // entry groups (of 16) per block of loads
+    constexpr int GU = 4;  // entry groups (of 16) per block of loads
     __shared__ uint32_t s_brow[kMmaWaves][kMmaPiece];
 
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -508,7 +508,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
     const int32_t ng = ne / kTileMmaGroup;
     int32_t g0 = 0;
     for (; g0 + GU <= ng; g0 += GU) block(std::integral_constant<int, GU>(), g0);
-    if (g0 < ng) block(std::integral_constant<int, 1>(), g0);
+    for (; g0 < ng; ++g0) block(std::integral_constant<int, 1>(), g0);
 
     // This lane holds rows 4*kq + v of the tile, columns col .. col+VEC-1.
     bool fin = true;
