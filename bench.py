@@ -97,7 +97,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
-    ap.add_argument("--algo", default="vcsr", choices=["vcsr", "tile", "row", "segment", "mfma", "csr"])
+    ap.add_argument("--algo", default="vcsr",
+                    choices=["vcsr", "tile", "row", "segment", "mfma", "csr", "rocsparse"])
     ap.add_argument("--tileK", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -148,7 +149,17 @@ def main():
     # Kernels that write every C element themselves need no reset per step;
     # the accumulate-into-C kernels get a C reset inside the timed step.
     needs_reset = True
-    if args.algo == "csr":
+    if args.algo == "rocsparse":
+        # The vendor baseline (rocSPARSE SpMM, C = A*B), set up once.
+        d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
+        d_col = vs.DeviceArray.from_numpy(csr.col, st)
+        d_val = vs.DeviceArray.from_numpy(csr.val, st)
+        plan = vs.VendorPlan(csr.M, csr.N, csr.nnz, d_rp, d_col, d_val, dB, O, dC, st)
+        needs_reset = False
+
+        def kernel(timed=False):
+            return plan.run(st, timed=timed)
+    elif args.algo == "csr":
         d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
         d_col = vs.DeviceArray.from_numpy(csr.col, st)
         d_val = vs.DeviceArray.from_numpy(csr.val, st)
@@ -242,7 +253,8 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{args.config}: {csr.M}x{csr.N} nnz={csr.nnz} O={O}",
                    "algo": args.algo, "segw": segw, "bundle": bundle, "tileK": tileK,
-                   "layout": ["H", "S", "TC"][layout] if args.algo != "csr" else "csr",
+                   "layout": ["H", "S", "TC"][layout] if args.algo not in ("csr", "rocsparse")
+                   else "csr",
                    "step": "C reset + SpMM kernel (C += A*B)" if needs_reset
                    else "SpMM kernel writing C = A*B"},
         "kernel_ms": round(kernel_ms, 5),

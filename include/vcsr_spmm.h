@@ -225,6 +225,27 @@ int vcsr_mfma_work(const vcsr_fmt* fmt, int32_t O, int32_t tileK, int64_t* ops,
  * No reference counterpart. */
 int vcsr_tile_mfma_work(const vcsr_fmt* fmt, int32_t O, int64_t* ops, int32_t* flops_per_op);
 
+/* ------------------------------------------------------ vendor baseline */
+/* rocSPARSE SpMM (CSR int32 x row-major dense, FP32, default algorithm,
+ * C = A*B) on caller-owned device arrays: the counterpart of
+ * run_cusparse_spmm (src/kernels.cu:169-235), for comparison only.
+ * vcsr_vendor_plan_create sets up the handle, descriptors and work buffer
+ * (the reference does this inside every call, outside its timed region) and
+ * binds the plan to these arrays; vcsr_vendor_spmm computes on `stream` and,
+ * if ms is non-NULL, waits and stores the time of the SpMM call alone.
+ * spmm_csr_vendor is the one-shot form with the reference's behaviour
+ * (returns after the computation).  Failures of the library are
+ * VCSR_EDEVICE with its status in vcsr_last_error(). */
+typedef struct vcsr_vendor_plan vcsr_vendor_plan;
+int vcsr_vendor_plan_create(int32_t M, int32_t N, int32_t nnz, const int32_t* rowptr,
+                            const int32_t* col, const float* val, const float* dB,
+                            int32_t O, float* dC, void* stream, vcsr_vendor_plan** out);
+int vcsr_vendor_spmm(vcsr_vendor_plan* plan, void* stream, float* ms);
+void vcsr_vendor_plan_free(vcsr_vendor_plan* plan);
+int spmm_csr_vendor(int32_t M, int32_t N, int32_t nnz, const int32_t* rowptr,
+                    const int32_t* col, const float* val, const float* dB, int32_t O,
+                    float* dC, void* stream, float* ms);
+
 /* CPU CSR SpMM, C = A*B in FP32, for each row: p ascending, k inner, one
  * fused multiply-add per term (the loop order of src/kernels.cu:25-32).
  * nthreads <= 0 uses every hardware thread (rows are independent, so the

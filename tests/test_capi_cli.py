@@ -70,8 +70,13 @@ def test_cli_usage_errors(vs):
     assert run_cli(vs).returncode == 1                       # no --mtx / --gen
     assert run_cli(vs, "--bogus").returncode == 1            # unknown option
     assert run_cli(vs, "--gen", "cfg1", "--algo", "nope").returncode == 1
-    r = run_cli(vs, "--gen", "cfg1", "--algo", "cusparse")
+    r = run_cli(vs, "--gen", "cfg1", "--algo", "aspt")
     assert r.returncode == 1 and "not part of this build" in r.stdout
+    # cusparse names the vendor baseline (rocSPARSE here), a GPU algorithm.
+    r = run_cli(vs, "--gen", "cfg1", "--algo", "cusparse")
+    assert r.returncode in (0, 2)
+    if r.returncode == 2:
+        assert "no GPU visible" in r.stderr
 
 
 def test_cli_cpu_line_format(vs, tmp_path):

@@ -414,3 +414,26 @@ def test_tile_mfma_work_counts_the_launch(gpu, orc, st, O):
     other.set_tile_rows(8)
     other.upload(st)
     assert vs.tile_mfma_work(other, O)[0] == 0
+
+
+@pytest.mark.parametrize("O", [1, 8, 33, 128])
+def test_vendor_baseline_matches_oracle(gpu, orc, st, O):
+    """The rocSPARSE baseline (one-shot and plan) computes C = A*B within the
+    north-star tolerance, overwriting C, on random and empty-row matrices."""
+    vs = gpu
+    rng = np.random.default_rng(O)
+    csr = _block_csr(vs, rng, 40, 3, 500, 9, 3, 0.7)
+    B = vs.gen_dense(O, 0, csr.N, O)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    rp, col, val = _device_csr(vs, csr, st)
+    dB = vs.DeviceArray.from_numpy(B, st)
+    dC = vs.DeviceArray.from_numpy(np.full((csr.M, O), 7.0, np.float32), st)
+    ms = vs.run_vendor_spmm_gpu(csr.M, csr.N, csr.nnz, rp, col, val, dB, O, dC, st, timed=True)
+    assert ms >= 0
+    assert_within_tolerance(dC.numpy(st), ref64, csr.row_ptr, csr.val, B, f"one-shot O{O}")
+    dC2 = vs.DeviceArray.from_numpy(np.full((csr.M, O), -3.0, np.float32), st)
+    plan = vs.VendorPlan(csr.M, csr.N, csr.nnz, rp, col, val, dB, O, dC2, st)
+    for _ in range(2):
+        plan.run(st)
+    st.sync()
+    assert_within_tolerance(dC2.numpy(st), ref64, csr.row_ptr, csr.val, B, f"plan O{O}")

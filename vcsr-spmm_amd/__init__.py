@@ -43,6 +43,7 @@ EXPORTS = (
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
     "vcsr_fmt_set_tile_rows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_vcsr "
     "spmm_vcsr_ex spmm_vcsr_mfma vcsr_mfma_work vcsr_tile_mfma_work spmm_csr_cpu "
+    "vcsr_vendor_plan_create vcsr_vendor_spmm vcsr_vendor_plan_free spmm_csr_vendor "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
     "vcsr_memcpy_d2h vcsr_memcpy_d2d vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
     "vcsr_stream_sync vcsr_device_sync vcsr_event_create vcsr_event_destroy "
@@ -117,6 +118,11 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "vcsr_mfma_work": (C.c_int, [P, I32, I32, C.POINTER(I64), pI]),
         "vcsr_tile_mfma_work": (C.c_int, [P, I32, C.POINTER(I64), pI]),
         "spmm_csr_cpu": (C.c_int, [I32, P, P, P, P, I32, P, I32]),
+        "vcsr_vendor_plan_create": (C.c_int, [I32, I32, I32, P, P, P, P, I32, P, P,
+                                              C.POINTER(P)]),
+        "vcsr_vendor_spmm": (C.c_int, [P, P, pF]),
+        "vcsr_vendor_plan_free": (None, [P]),
+        "spmm_csr_vendor": (C.c_int, [I32, I32, I32, P, P, P, P, I32, P, P, pF]),
         "vcsr_device_count": (C.c_int, [pI]),
         "vcsr_device_name": (C.c_int, [C.c_char_p, I32]),
         "vcsr_dev_malloc": (C.c_int, [pP, C.c_size_t]),
@@ -410,6 +416,41 @@ def run_csr_spmm_gpu(M, d_rowptr, d_col, d_val, dB, O, dC, stream=None, timed=Fa
     ms = C.c_float(0)
     _check(load_library().spmm_csr_naive(M, d_rowptr.ptr, d_col.ptr, d_val.ptr, dB.ptr, O,
                                          dC.ptr, _sp(stream), C.byref(ms) if timed else None))
+    return ms.value if timed else None
+
+
+class VendorPlan:
+    """rocSPARSE SpMM (C = A*B) bound to device CSR arrays, B and C: the
+    vendor baseline (the reference's run_cusparse_spmm, src/kernels.cu:169-235)
+    with its set-up done once."""
+
+    def __init__(self, M, N, nnz, d_rowptr, d_col, d_val, dB, O, dC, stream=None):
+        h = C.c_void_p()
+        _check(load_library().vcsr_vendor_plan_create(M, N, nnz, d_rowptr.ptr, d_col.ptr,
+                                                      d_val.ptr, dB.ptr, O, dC.ptr, _sp(stream),
+                                                      C.byref(h)))
+        self._h = h
+        self._keep = (d_rowptr, d_col, d_val, dB, dC)
+
+    def run(self, stream=None, timed=False):
+        """C = A*B; the SpMM call's ms when timed (synchronous)."""
+        ms = C.c_float(0)
+        _check(load_library().vcsr_vendor_spmm(self._h, _sp(stream),
+                                               C.byref(ms) if timed else None))
+        return ms.value if timed else None
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            load_library().vcsr_vendor_plan_free(self._h)
+            self._h = C.c_void_p()
+
+
+def run_vendor_spmm_gpu(M, N, nnz, d_rowptr, d_col, d_val, dB, O, dC, stream=None, timed=False):
+    """One-shot rocSPARSE C = A*B (set-up, SpMM, tear-down, like the
+    reference's cuSPARSE wrapper); the SpMM call's ms when timed."""
+    ms = C.c_float(0)
+    _check(load_library().spmm_csr_vendor(M, N, nnz, d_rowptr.ptr, d_col.ptr, d_val.ptr, dB.ptr,
+                                          O, dC.ptr, _sp(stream), C.byref(ms) if timed else None))
     return ms.value if timed else None
 
 
