@@ -98,7 +98,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--algo", default="vcsr",
-                    choices=["vcsr", "tile", "row", "segment", "mfma", "csr", "rocsparse"])
+                    choices=["vcsr", "tile", "row", "segment", "mfma", "csr", "aspt", "rocsparse"])
     ap.add_argument("--tileK", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -159,6 +159,16 @@ def main():
 
         def kernel(timed=False):
             return plan.run(st, timed=timed)
+    elif args.algo == "aspt":
+        # Wave-per-row CSR on the plain CSR arrays (overwrites C).
+        d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
+        d_col = vs.DeviceArray.from_numpy(csr.col, st)
+        d_val = vs.DeviceArray.from_numpy(csr.val, st)
+        needs_reset = False
+
+        def kernel(timed=False):
+            return vs.run_csr_wave_spmm_gpu(csr.M, csr.N, d_rp, d_col, d_val, dB, O, dC, st,
+                                            timed=timed)
     elif args.algo == "csr":
         d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
         d_col = vs.DeviceArray.from_numpy(csr.col, st)
@@ -253,7 +263,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{args.config}: {csr.M}x{csr.N} nnz={csr.nnz} O={O}",
                    "algo": args.algo, "segw": segw, "bundle": bundle, "tileK": tileK,
-                   "layout": ["H", "S", "TC"][layout] if args.algo not in ("csr", "rocsparse")
+                   "layout": ["H", "S", "TC"][layout] if args.algo not in ("csr", "aspt", "rocsparse")
                    else "csr",
                    "step": "C reset + SpMM kernel (C += A*B)" if needs_reset
                    else "SpMM kernel writing C = A*B"},

@@ -164,6 +164,16 @@ int spmm_csr_naive(int32_t M, const int32_t* d_rowptr, const int32_t* d_col,
                    const float* d_val, const float* dB, int32_t O, float* dC,
                    void* stream, float* ms);
 
+/* C = A*B on plain CSR with rows spread over the lanes of a wavefront: each
+ * row's (column, value) pairs are read once and shared by its lanes, C is
+ * written once (overwritten; no reset needed).  The ASpT-style competitor:
+ * replaces run_aspt_spmm_gpu (src/aspt.cu:144-196), which needs O % 64 == 0;
+ * this takes any O and one more argument, N (the rows of B), which bounds
+ * B's addressing: a column outside [0, N) contributes nothing. */
+int spmm_csr_wave(int32_t M, int32_t N, const int32_t* rowptr, const int32_t* col,
+                  const float* val, const float* dB, int32_t O, float* dC, void* stream,
+                  float* ms);
+
 /* C += A*B over an uploaded VCSR format (any layout) with the fastest kernel
  * (VCSR_KERNEL_AUTO).  C is accumulated into: zero it first, as
  * main.cpp:126-143 does.  tileK is the C/B column tile of the segment-major

@@ -437,3 +437,58 @@ def test_vendor_baseline_matches_oracle(gpu, orc, st, O):
         plan.run(st)
     st.sync()
     assert_within_tolerance(dC2.numpy(st), ref64, csr.row_ptr, csr.val, B, f"plan O{O}")
+
+
+def _run_wave(vs, st, M, N, row_ptr, col, val, B):
+    rp = vs.DeviceArray.from_numpy(np.ascontiguousarray(row_ptr, np.int32), st)
+    dcol = vs.DeviceArray.from_numpy(np.ascontiguousarray(col, np.int32), st)
+    dval = vs.DeviceArray.from_numpy(np.ascontiguousarray(val, np.float32), st)
+    dB = vs.DeviceArray.from_numpy(B, st)
+    dC = vs.DeviceArray.from_numpy(np.full((M, B.shape[1]), 5.0, np.float32), st)
+    vs.run_csr_wave_spmm_gpu(M, N, rp, dcol, dval, dB, B.shape[1], dC, st, timed=True)
+    return dC.numpy(st)
+
+
+@pytest.mark.parametrize("O", [1, 7, 32, 128, 130, 300])
+def test_csr_wave_bit_exact_random(gpu, orc, st, O):
+    """The wave-per-row CSR kernel applies each row's entries in CSR order
+    with one fused multiply-add per term, like the oracle: bit-exact, with
+    duplicates and empty rows; C is overwritten."""
+    vs = gpu
+    rng = np.random.default_rng(200 + O)
+    csr = _case(vs, orc, rng, 300, 257, density=0.04, dup_rate=0.1, empty_rows=0.1)
+    B = vs.gen_dense(9, 0, csr.N, O)
+    C = _run_wave(vs, st, csr.M, csr.N, csr.row_ptr, csr.col, csr.val, B)
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))
+
+
+def test_csr_wave_bit_exact_power_law(gpu, orc, st):
+    """cfg3 (rows up to ~17k entries, many rows per wave at O = 8)."""
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(3, 0))
+    B = vs.gen_dense(3, 0, csr.N, 8)
+    C = _run_wave(vs, st, csr.M, csr.N, csr.row_ptr, csr.col, csr.val, B)
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))
+
+
+def test_csr_wave_ignores_columns_outside_b(gpu, orc, st):
+    """Columns outside [0, N) contribute nothing (the kernel bounds B's
+    addressing by N): the result equals the CSR without those entries."""
+    vs = gpu
+    rng = np.random.default_rng(5)
+    M, N, O = 50, 40, 64
+    lens = rng.integers(0, 12, M)
+    row_ptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    col = rng.integers(0, N, row_ptr[-1]).astype(np.int32)
+    bad = rng.random(col.size) < 0.2
+    col[bad] = np.where(rng.random(bad.sum()) < 0.5, -3, N + 7)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    B = vs.gen_dense(1, 0, N, O)
+    C = _run_wave(vs, st, M, N, row_ptr, col, val, B)
+    keep = ~bad
+    rp2 = np.concatenate([[0], np.cumsum([keep[row_ptr[r]:row_ptr[r + 1]].sum()
+                                          for r in range(M)])]).astype(np.int32)
+    ref = orc.spmm_f32(M, rp2, col[keep], val[keep], B)
+    assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))

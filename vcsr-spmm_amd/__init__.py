@@ -41,7 +41,7 @@ EXPORTS = (
     "vcsr_last_error vcsr_version vcsr_mtx_read vcsr_coo_create vcsr_coo_view_get "
     "vcsr_coo_free vcsr_gen_coo vcsr_gen_dense vcsr_coo_to_csr vcsr_csr_create "
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
-    "vcsr_fmt_set_tile_rows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_vcsr "
+    "vcsr_fmt_set_tile_rows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_csr_wave spmm_vcsr "
     "spmm_vcsr_ex spmm_vcsr_mfma vcsr_mfma_work vcsr_tile_mfma_work spmm_csr_cpu "
     "vcsr_vendor_plan_create vcsr_vendor_spmm vcsr_vendor_plan_free spmm_csr_vendor "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
@@ -112,6 +112,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "vcsr_fmt_tile_info": (C.c_int, [P, pI, C.POINTER(I64), C.POINTER(I64)]),
         "vcsr_fmt_free": (None, [P]),
         "spmm_csr_naive": (C.c_int, [I32, P, P, P, P, I32, P, P, pF]),
+        "spmm_csr_wave": (C.c_int, [I32, I32, P, P, P, P, I32, P, P, pF]),
         "spmm_vcsr": (C.c_int, [P, P, I32, I32, P, P, pF]),
         "spmm_vcsr_ex": (C.c_int, [P, P, I32, I32, P, P, pF, I32, I32]),
         "spmm_vcsr_mfma": (C.c_int, [P, P, I32, P, P, pF]),
@@ -451,6 +452,15 @@ def run_vendor_spmm_gpu(M, N, nnz, d_rowptr, d_col, d_val, dB, O, dC, stream=Non
     ms = C.c_float(0)
     _check(load_library().spmm_csr_vendor(M, N, nnz, d_rowptr.ptr, d_col.ptr, d_val.ptr, dB.ptr,
                                           O, dC.ptr, _sp(stream), C.byref(ms) if timed else None))
+    return ms.value if timed else None
+
+
+def run_csr_wave_spmm_gpu(M, N, d_rowptr, d_col, d_val, dB, O, dC, stream=None, timed=False):
+    """C = A*B with the wave-per-row CSR kernel (overwrites C); kernel ms
+    when timed (synchronous)."""
+    ms = C.c_float(0)
+    _check(load_library().spmm_csr_wave(M, N, d_rowptr.ptr, d_col.ptr, d_val.ptr, dB.ptr, O,
+                                        dC.ptr, _sp(stream), C.byref(ms) if timed else None))
     return ms.value if timed else None
 
 

@@ -9,8 +9,9 @@
 // vcsr_baseline and vcsr_seg, the reference's names at main.cpp:135-146),
 // vcsr_mfma (FP32-MFMA dense-block kernel on the same format), vcsr_tc
 // (layout TC, segw=16 bundle=16, on the MFMA kernel), rocsparse (the vendor
-// baseline; alias cusparse, the reference's name at main.cpp:119-123), cpu,
-// all.
+// baseline; alias cusparse, the reference's name at main.cpp:119-123), aspt
+// (wave-per-row CSR, the reference's ASpT competitor at main.cpp:153-157),
+// cpu, all.
 //
 // Result lines keep the format of the published runs, which the reference's
 // bench scripts parse (token before "ms" and before "GFLOP/s" on the last
@@ -51,7 +52,7 @@ void usage() {
     std::printf("Options: --segw w --bundle b --tileK t --repeat r --warmup w --seed s\n");
     std::printf("         --layout H|S --check --threads T --expand-symmetric\n");
     std::printf("Algorithms: csr, vcsr (vcsr_baseline, vcsr_seg), vcsr_mfma, vcsr_tc, "
-                "rocsparse (cusparse), cpu, all\n");
+                "rocsparse (cusparse), aspt, cpu, all\n");
 }
 
 [[noreturn]] void die(const char* what, int rc) {
@@ -143,13 +144,13 @@ int main(int argc, char** argv) {
     if (o.O <= 0 || o.repeat <= 0 || o.warmup < 0) { usage(); return 1; }
     if (o.algo == "vcsr_baseline" || o.algo == "vcsr_seg") o.algo = "vcsr";
     if (o.algo == "cusparse") o.algo = "rocsparse";
-    if (o.algo == "aspt" || o.algo == "fast" || o.algo == "fastspmm" || o.algo == "vcsr_naive") {
+    if (o.algo == "fast" || o.algo == "fastspmm" || o.algo == "vcsr_naive") {
         std::printf("%s: not part of this build (vendor or competitor kernel)\n", o.algo.c_str());
         return 1;
     }
     const bool all = o.algo == "all";
     if (!all && o.algo != "csr" && o.algo != "vcsr" && o.algo != "vcsr_mfma" &&
-        o.algo != "vcsr_tc" && o.algo != "rocsparse" && o.algo != "cpu") {
+        o.algo != "vcsr_tc" && o.algo != "rocsparse" && o.algo != "aspt" && o.algo != "cpu") {
         usage();
         return 1;
     }
@@ -265,6 +266,20 @@ int main(int argc, char** argv) {
         report_check("rocsparse");
         report_roofline(sum / o.repeat);
         std::printf("%-12s%8.3f ms %9.2f GFLOP/s  (vendor)\n", "rocSPARSE:", sum / o.repeat,
+                    gflops(sum / o.repeat));
+    }
+    if (all || o.algo == "aspt") {
+        float ms = 0, sum = 0;
+        for (int it = 0; it < o.warmup; ++it)
+            CHECK(spmm_csr_wave(A.M, A.N, drp, dcol, dval, dB, O, dC, st, &ms));
+        for (int it = 0; it < o.repeat; ++it) {
+            CHECK(vcsr_memset_d(dC, 0, bytesC, st));
+            CHECK(spmm_csr_wave(A.M, A.N, drp, dcol, dval, dB, O, dC, st, &ms));
+            sum += ms;
+        }
+        report_check("aspt");
+        report_roofline(sum / o.repeat);
+        std::printf("%-12s%8.3f ms %9.2f GFLOP/s\n", "ASpT (wave):", sum / o.repeat,
                     gflops(sum / o.repeat));
     }
     if (all || o.algo == "csr") {

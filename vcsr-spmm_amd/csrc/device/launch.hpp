@@ -15,6 +15,11 @@ hipError_t launch_csr_naive(int32_t M, const int32_t* rowptr, const int32_t* col
                             const float* val, const float* B, int32_t O, float* C,
                             hipStream_t st);
 
+// csr_wave.hip: C = A*B on plain CSR, rows spread over wavefront lanes
+// (the ASpT-style competitor).  N bounds B's addressing.
+hipError_t launch_csr_wave(int32_t M, const int32_t* rowptr, const int32_t* col, const float* val,
+                           const float* B, int32_t N, int32_t O, float* C, hipStream_t st);
+
 // vcsr_stream.hip: C += A*B, VCSR segmented streaming on the vector ALUs.
 hipError_t launch_vcsr_stream(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                               int32_t tileK, float* C, hipStream_t st);

@@ -217,6 +217,20 @@ int spmm_csr_naive(int32_t M, const int32_t* d_rowptr, const int32_t* d_col, con
     });
 }
 
+int spmm_csr_wave(int32_t M, int32_t N, const int32_t* d_rowptr, const int32_t* d_col,
+                  const float* d_val, const float* dB, int32_t O, float* dC, void* stream,
+                  float* ms) {
+    return guarded([&] {
+        need(M >= 0 && N >= 0 && O >= 0, "negative shape");
+        need(M == 0 || O == 0 || (d_rowptr && dC), "null pointer");
+        need_device();
+        run_timed((hipStream_t)stream, ms, [&] {
+            return vcsr::launch_csr_wave(M, d_rowptr, d_col, d_val, dB, N, O, dC,
+                                         (hipStream_t)stream);
+        });
+    });
+}
+
 int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK, float* dC,
                  void* stream, float* ms, int32_t kernel, int32_t accumulate) {
     return guarded([&] {
