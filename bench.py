@@ -98,7 +98,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--algo", default="vcsr",
-                    choices=["vcsr", "tile", "row", "segment", "mfma", "csr", "aspt", "rocsparse"])
+                    choices=["vcsr", "tile", "row", "segment", "mfma", "fast", "csr", "aspt",
+                             "rocsparse"])
     ap.add_argument("--tileK", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -180,6 +181,10 @@ def main():
     else:
         t0 = time.perf_counter()
         fmt = vs.build_vcsr(csr, segw, bundle, layout)
+        if args.algo == "fast":
+            # FastSpMM's layout: fixed 16-row windows of condensed columns.
+            fmt.set_tile_rows(16)
+            fmt.set_tile_windows(True)
         tb = time.perf_counter() - t0
         t0 = time.perf_counter()
         fmt.upload(st)
@@ -189,7 +194,8 @@ def main():
         log(f"bench: row-tile view: {tt} tiles of <= {tr} rows, {te} entries "
             f"({csr.nnz / max(te, 1):.2f} nonzeros per B-row load)")
         kern = {"vcsr": vs.KERNEL_AUTO, "tile": vs.KERNEL_TILE, "row": vs.KERNEL_ROW,
-                "segment": vs.KERNEL_SEGMENT, "mfma": vs.KERNEL_MFMA}[args.algo]
+                "segment": vs.KERNEL_SEGMENT, "mfma": vs.KERNEL_MFMA,
+                "fast": vs.KERNEL_TILE}[args.algo]
         overwrite = kern in (vs.KERNEL_AUTO, vs.KERNEL_TILE, vs.KERNEL_ROW)
         needs_reset = not overwrite
 
@@ -276,7 +282,7 @@ def main():
                      "bytes_alg": bytes_alg},
     }
     # The tile-stationary kernel runs 16-row tiles on the matrix cores.
-    tile_mma = args.algo in ("vcsr", "tile") and tr == 16
+    tile_mma = args.algo in ("vcsr", "tile", "fast") and tr == 16
     if args.algo == "mfma" or tile_mma:
         # Matrix-core utilisation: issued MFMA FLOPs (dense group tiles or
         # 16-row tiles, padding included) per kernel time against the dense

@@ -142,6 +142,14 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream);
  * the FP32 matrix cores (dense sub-blocks, layout TC matrices).  Only before
  * the upload (VCSR_ESTATE after).  No reference counterpart. */
 int vcsr_fmt_set_tile_rows(vcsr_fmt* fmt, int32_t rows);
+/* fixed != 0: cut the rows into fixed windows of the tile height (which must
+ * then be set) instead of tiles of rows that share columns.  With 16
+ * rows this is FastSpMM's condensed-tile layout (16-row windows whose
+ * distinct columns form 16-column blocks; build_cst_from_csr,
+ * src/fastspmm.cu:129-233), computed on FP32 MFMA instead of FP16 WMMA
+ * (run_fastspmm_gpu, src/fastspmm.cu:257-303).  Only before the upload
+ * (VCSR_ESTATE after); an upload without a tile height is VCSR_EINVAL. */
+int vcsr_fmt_set_tile_windows(vcsr_fmt* fmt, int32_t fixed);
 /* The uploaded view's tile height, tile count and entry count (B-row slice
  * loads per column tile of one SpMM; nnz for tile height 1).  No reference
  * counterpart. */

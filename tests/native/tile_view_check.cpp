@@ -30,9 +30,10 @@ static int fail(const char* what, int M, int R) {
     return 1;
 }
 
-static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, int expect_R) {
+static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, int expect_R,
+                 bool fixed = false) {
     const Vcsr v = build_vcsr(csr, segw, bundle, layout, 2);
-    const TileView tv = make_tile_view(v, R_req, 2);
+    const TileView tv = make_tile_view(v, R_req, 2, fixed);
     const int R = tv.R, RS = tile_slot_stride(R), M = csr.M;
     if (expect_R > 0 && R != expect_R) return fail("tile height", M, R);
     const int64_t E = tv.n_entries();
@@ -99,6 +100,8 @@ static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, in
                 got.emplace_back(row0 + r, tv.brow[q], a);
             }
         }
+        if (fixed && (row0 % R != 0 || nr != std::min(R, M - row0)))
+            return fail("fixed window not aligned or not full", M, R);
         if (tv.pieces[4 * p + 3] < 0)
             for (int r = 0; r < nr; ++r) covered[(size_t)(row0 + r)]++;
     }
@@ -181,6 +184,11 @@ int main() {
         bad |= check(block_matrix(8, 30, 3, 300, 7, 3, 75, true), 4, 64, layout, 16, 16);
     }
     bad |= check(cfg1, 4, 64, kLayoutS, 16, 16);
+    // Fixed row windows (16 rows: FastSpMM's condensed tiles), any matrix.
+    bad |= check(cfg1, 4, 64, kLayoutS, 16, 16, true);
+    bad |= check(block_matrix(9, 30, 3, 300, 7, 3, 75, true), 4, 64, kLayoutS, 16, 16, true);
+    bad |= check(block_matrix(9, 30, 3, 300, 7, 3, 75, true), 4, 64, kLayoutH, 4, 4, true);
+    bad |= check(block_matrix(37, 4, 16, 8192, 700, 4, 90, false), 4, 64, kLayoutS, 16, 16, true);
     // Tiles wider than one work item (split into pieces with partial sums).
     for (int R : {1, 3, 8}) bad |= check(block_matrix(20 + R, 6, 8, 4096, 300, 4, 90, false), 4, 64, kLayoutS, R, R);
     bad |= check(block_matrix(36, 4, 16, 8192, 700, 4, 90, false), 4, 64, kLayoutS, 16, 16);

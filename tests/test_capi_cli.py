@@ -70,7 +70,7 @@ def test_cli_usage_errors(vs):
     assert run_cli(vs).returncode == 1                       # no --mtx / --gen
     assert run_cli(vs, "--bogus").returncode == 1            # unknown option
     assert run_cli(vs, "--gen", "cfg1", "--algo", "nope").returncode == 1
-    r = run_cli(vs, "--gen", "cfg1", "--algo", "fast")
+    r = run_cli(vs, "--gen", "cfg1", "--algo", "vcsr_naive")
     assert r.returncode == 1 and "not part of this build" in r.stdout
     # cusparse names the vendor baseline (rocSPARSE here), a GPU algorithm.
     r = run_cli(vs, "--gen", "cfg1", "--algo", "cusparse")

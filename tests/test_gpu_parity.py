@@ -492,3 +492,28 @@ def test_csr_wave_ignores_columns_outside_b(gpu, orc, st):
                                           for r in range(M)])]).astype(np.int32)
     ref = orc.spmm_f32(M, rp2, col[keep], val[keep], B)
     assert np.array_equal(C.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("tile_rows", [4, 16])
+@pytest.mark.parametrize("O", [8, 64, 200])
+def test_fixed_row_windows(gpu, orc, st, tile_rows, O):
+    """Fixed row windows (16 rows: FastSpMM's condensed-tile layout) on a
+    matrix whose rows share few columns, with empty and duplicate entries:
+    C = A*B and C += A*B within the north-star tolerance."""
+    vs = gpu
+    rng = np.random.default_rng(tile_rows * 1000 + O)
+    csr = _case(vs, orc, rng, 333, 290, density=0.03, dup_rate=0.05, empty_rows=0.1)
+    B = vs.gen_dense(O + 1, 0, csr.N, O)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.set_tile_rows(tile_rows)
+    fmt.set_tile_windows(True)
+    fmt.upload(st)
+    R, tiles, entries = fmt.tile_info()
+    assert R == tile_rows and tiles == -(-csr.M // tile_rows)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    C0 = rng.uniform(-1, 1, size=(csr.M, O)).astype(np.float32)
+    for accumulate in (False, True):
+        got = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate)
+        if accumulate:
+            got = got - C0
+        assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"R{R} O{O}")

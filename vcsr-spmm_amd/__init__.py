@@ -41,7 +41,7 @@ EXPORTS = (
     "vcsr_last_error vcsr_version vcsr_mtx_read vcsr_coo_create vcsr_coo_view_get "
     "vcsr_coo_free vcsr_gen_coo vcsr_gen_dense vcsr_coo_to_csr vcsr_csr_create "
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
-    "vcsr_fmt_set_tile_rows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_csr_wave spmm_vcsr "
+    "vcsr_fmt_set_tile_rows vcsr_fmt_set_tile_windows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_csr_wave spmm_vcsr "
     "spmm_vcsr_ex spmm_vcsr_mfma vcsr_mfma_work vcsr_tile_mfma_work spmm_csr_cpu "
     "vcsr_vendor_plan_create vcsr_vendor_spmm vcsr_vendor_plan_free spmm_csr_vendor "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
@@ -109,6 +109,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "vcsr_fmt_arrays": (C.c_int, [P, C.POINTER(_Arrays)]),
         "vcsr_fmt_upload": (C.c_int, [P, P]),
         "vcsr_fmt_set_tile_rows": (C.c_int, [P, I32]),
+        "vcsr_fmt_set_tile_windows": (C.c_int, [P, I32]),
         "vcsr_fmt_tile_info": (C.c_int, [P, pI, C.POINTER(I64), C.POINTER(I64)]),
         "vcsr_fmt_free": (None, [P]),
         "spmm_csr_naive": (C.c_int, [I32, P, P, P, P, I32, P, P, pF]),
@@ -288,6 +289,11 @@ class Vcsr:
     def set_tile_rows(self, rows: int) -> None:
         """Tile height of the row-tile view (0 = automatic); before upload()."""
         _check(load_library().vcsr_fmt_set_tile_rows(self._h, rows))
+
+    def set_tile_windows(self, fixed: bool) -> None:
+        """Fixed row windows of the tile height instead of shared-column
+        tiles (16 rows: FastSpMM's condensed tiles); before upload()."""
+        _check(load_library().vcsr_fmt_set_tile_windows(self._h, 1 if fixed else 0))
 
     def tile_info(self) -> tuple[int, int, int]:
         """(tile height, tiles, entries) of the uploaded row-tile view."""

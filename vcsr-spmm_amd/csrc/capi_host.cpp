@@ -219,6 +219,14 @@ int vcsr_fmt_set_tile_rows(vcsr_fmt* fmt, int32_t rows) {
     });
 }
 
+int vcsr_fmt_set_tile_windows(vcsr_fmt* fmt, int32_t fixed) {
+    return guarded([&] {
+        need(fmt != nullptr, "null format");
+        if (fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format already uploaded");
+        fmt->tile_fixed = fixed != 0;
+    });
+}
+
 int vcsr_fmt_tile_info(const vcsr_fmt* fmt, int32_t* rows, int64_t* tiles, int64_t* entries) {
     return guarded([&] {
         need(fmt != nullptr, "null format");

@@ -11,7 +11,8 @@
 // (layout TC, segw=16 bundle=16, on the MFMA kernel), rocsparse (the vendor
 // baseline; alias cusparse, the reference's name at main.cpp:119-123), aspt
 // (wave-per-row CSR, the reference's ASpT competitor at main.cpp:153-157),
-// cpu, all.
+// fast (alias fastspmm: FastSpMM's fixed 16-row windows of condensed
+// columns, main.cpp:158-162, on the FP32-MFMA tile kernel), cpu, all.
 //
 // Result lines keep the format of the published runs, which the reference's
 // bench scripts parse (token before "ms" and before "GFLOP/s" on the last
@@ -52,7 +53,7 @@ void usage() {
     std::printf("Options: --segw w --bundle b --tileK t --repeat r --warmup w --seed s\n");
     std::printf("         --layout H|S --check --threads T --expand-symmetric\n");
     std::printf("Algorithms: csr, vcsr (vcsr_baseline, vcsr_seg), vcsr_mfma, vcsr_tc, "
-                "rocsparse (cusparse), aspt, cpu, all\n");
+                "rocsparse (cusparse), aspt, fast (fastspmm), cpu, all\n");
 }
 
 [[noreturn]] void die(const char* what, int rc) {
@@ -144,13 +145,15 @@ int main(int argc, char** argv) {
     if (o.O <= 0 || o.repeat <= 0 || o.warmup < 0) { usage(); return 1; }
     if (o.algo == "vcsr_baseline" || o.algo == "vcsr_seg") o.algo = "vcsr";
     if (o.algo == "cusparse") o.algo = "rocsparse";
-    if (o.algo == "fast" || o.algo == "fastspmm" || o.algo == "vcsr_naive") {
+    if (o.algo == "fastspmm") o.algo = "fast";
+    if (o.algo == "vcsr_naive") {
         std::printf("%s: not part of this build (vendor or competitor kernel)\n", o.algo.c_str());
         return 1;
     }
     const bool all = o.algo == "all";
     if (!all && o.algo != "csr" && o.algo != "vcsr" && o.algo != "vcsr_mfma" &&
-        o.algo != "vcsr_tc" && o.algo != "rocsparse" && o.algo != "aspt" && o.algo != "cpu") {
+        o.algo != "vcsr_tc" && o.algo != "rocsparse" && o.algo != "aspt" && o.algo != "fast" &&
+        o.algo != "cpu") {
         usage();
         return 1;
     }
@@ -296,10 +299,17 @@ int main(int argc, char** argv) {
         std::printf("%-12s%8.3f ms %9.2f GFLOP/s\n", "CSR (naive):", sum / o.repeat,
                     gflops(sum / o.repeat));
     }
-    auto run_vcsr = [&](const char* label, int lay, int segw, int bundle, bool mfma) {
+    // kind: 0 = spmm_vcsr (tile kernel), 1 = spmm_vcsr_mfma (group dense
+    // tiles), 2 = spmm_vcsr on fixed 16-row windows (FastSpMM's layout).
+    auto run_vcsr = [&](const char* label, int lay, int segw, int bundle, int kind) {
+        const bool mfma = kind == 1;
         vcsr_fmt* fmt = nullptr;
         const double t0 = now_ms();
         CHECK(vcsr_build(csr, segw, bundle, lay, o.threads, &fmt));
+        if (kind == 2) {
+            CHECK(vcsr_fmt_set_tile_rows(fmt, 16));
+            CHECK(vcsr_fmt_set_tile_windows(fmt, 1));
+        }
         const double tb = now_ms() - t0;
         vcsr_arrays v;
         CHECK(vcsr_fmt_arrays(fmt, &v));
@@ -346,9 +356,10 @@ int main(int argc, char** argv) {
                     v.num_groups);
         vcsr_fmt_free(fmt);
     };
-    if (all || o.algo == "vcsr") run_vcsr("VCSR (seg):", layout, o.segw, o.bundle, false);
-    if (all || o.algo == "vcsr_mfma") run_vcsr("VCSR-MFMA:", layout, o.segw, o.bundle, true);
-    if (all || o.algo == "vcsr_tc") run_vcsr("VCSR-TC:", VCSR_LAYOUT_TC, 16, 16, true);
+    if (all || o.algo == "vcsr") run_vcsr("VCSR (seg):", layout, o.segw, o.bundle, 0);
+    if (all || o.algo == "vcsr_mfma") run_vcsr("VCSR-MFMA:", layout, o.segw, o.bundle, 1);
+    if (all || o.algo == "vcsr_tc") run_vcsr("VCSR-TC:", VCSR_LAYOUT_TC, 16, 16, 1);
+    if (all || o.algo == "fast") run_vcsr("FastSpMM:", layout, o.segw, o.bundle, 2);
 
     if (want_gpu) {
         vcsr_dev_free(dB);

@@ -159,7 +159,7 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
         }
         std::vector<int32_t> items = make_items(v, 256);
         RowView rv = make_row_view(v, nact);
-        const vcsr::TileView tv = vcsr::make_tile_view(v, fmt->tile_rows, 0);
+        const vcsr::TileView tv = vcsr::make_tile_view(v, fmt->tile_rows, 0, fmt->tile_fixed);
         DeviceFmt d;
         hip_check(hipGetDevice(&d.device), "hipGetDevice");
         try {

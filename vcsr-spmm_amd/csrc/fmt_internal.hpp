@@ -65,6 +65,7 @@ struct vcsr_fmt {
     vcsr::Vcsr v;
     DeviceFmt dev;
     int32_t tile_rows = 0;  // requested tile height of the row-tile view (0 = automatic)
+    bool tile_fixed = false;  // fixed windows of tile_rows rows instead of shared-column tiles
     int64_t tv_tiles = 0;   // tiles of the uploaded view
 };
 

@@ -112,8 +112,10 @@ struct Tile {
 
 // Greedy tiles of at most `cap` consecutive rows inside [r0, r1): the next
 // row joins the tile while at least half of its columns are already in the
-// tile's union (empty rows always join).
-void tile_rows(const RowLists& rl, int32_t r0, int32_t r1, int32_t cap, std::vector<Tile>& out) {
+// tile's union (empty rows always join).  With `fixed`, every tile is the
+// next `cap` rows whatever their columns (fixed row windows).
+void tile_rows(const RowLists& rl, int32_t r0, int32_t r1, int32_t cap, bool fixed,
+               std::vector<Tile>& out) {
     std::vector<int32_t> u, w;
     int32_t i = r0;
     while (i < r1) {
@@ -123,7 +125,7 @@ void tile_rows(const RowLists& rl, int32_t r0, int32_t r1, int32_t cap, std::vec
             const int32_t r = i + n;
             const size_t len = (size_t)(rl.ptr[(size_t)r + 1] - rl.ptr[(size_t)r]);
             union_into(u, rl.col.data() + rl.ptr[(size_t)r], len, w);
-            if ((w.size() - u.size()) * 2 > len) break;
+            if (!fixed && (w.size() - u.size()) * 2 > len) break;
             u.swap(w);
             ++n;
         }
@@ -132,13 +134,14 @@ void tile_rows(const RowLists& rl, int32_t r0, int32_t r1, int32_t cap, std::vec
     }
 }
 
-std::vector<Tile> make_tiles(const RowLists& rl, int32_t M, int32_t cap, int nthreads) {
+std::vector<Tile> make_tiles(const RowLists& rl, int32_t M, int32_t cap, bool fixed,
+                             int nthreads) {
     const int32_t nblk = (M + kTileRowBlock - 1) / kTileRowBlock;
     std::vector<std::vector<Tile>> per((size_t)nblk);
     parallel_for(nblk, 1, nthreads, [&](int64_t bb, int64_t be) {
         for (int64_t blk = bb; blk < be; ++blk) {
             const int32_t r0 = (int32_t)blk * kTileRowBlock;
-            tile_rows(rl, r0, std::min(M, r0 + kTileRowBlock), cap, per[(size_t)blk]);
+            tile_rows(rl, r0, std::min(M, r0 + kTileRowBlock), cap, fixed, per[(size_t)blk]);
         }
     });
     std::vector<Tile> tiles;
@@ -148,9 +151,10 @@ std::vector<Tile> make_tiles(const RowLists& rl, int32_t M, int32_t cap, int nth
 
 }  // namespace
 
-TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
+TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads, bool fixed) {
     if (R != 0 && R != 1 && R != 2 && R != 3 && R != 4 && R != 8 && R != kTileMmaRows)
         throw Error(kEinval, "tile height must be 0, 1, 2, 3, 4, 8 or 16");
+    if (fixed && R == 0) throw Error(kEinval, "fixed row windows need a tile height");
     if (nthreads <= 0) nthreads = default_threads();
     const int32_t M = v.M;
     const RowLists rl = row_lists(v, nthreads);
@@ -168,7 +172,7 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
     if (R == 0) {
         double best = 0;
         for (int32_t cap : {1, 2, 3, 4, 8, kTileMmaRows}) {
-            std::vector<Tile> t = make_tiles(rl, M, cap, nthreads);
+            std::vector<Tile> t = make_tiles(rl, M, cap, false, nthreads);
             int64_t ent = 0;
             for (const Tile& x : t) ent += pad(cap, x.nent);
             if (cap == kTileMmaRows && (int64_t)t.size() * 12 > (int64_t)M) continue;
@@ -182,7 +186,7 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads) {
             if (cap == 2 && R == 1) break;
         }
     } else {
-        tiles = make_tiles(rl, M, R, nthreads);
+        tiles = make_tiles(rl, M, R, fixed, nthreads);
     }
     if (R == kTileMmaRows)
         for (Tile& x : tiles) x.nent = pad(R, x.nent);

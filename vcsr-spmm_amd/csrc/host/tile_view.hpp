@@ -91,7 +91,11 @@ struct TileView {
 
 // Builds the view.  R = 0 picks the tile height that minimises the modelled
 // cost (B-row loads plus accumulator updates); R = 1, 2, 3, 4, 8 or 16 forces
-// it.
-TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads);
+// it.  fixed = true cuts the rows into fixed windows of R consecutive rows
+// (aligned to multiples of R from row 0 when R divides kTileRowBlock)
+// instead of growing a tile only over rows that share its columns; with
+// R = 16 that is the condensed-tile layout of FastSpMM (16-row windows whose
+// distinct columns form 16-column blocks, src/fastspmm.cu:129-253).
+TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads, bool fixed = false);
 
 }  // namespace vcsr
