@@ -517,3 +517,55 @@ def test_fixed_row_windows(gpu, orc, st, tile_rows, O):
         if accumulate:
             got = got - C0
         assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"R{R} O{O}")
+
+
+class _Shifted:
+    """A device buffer viewed `off` bytes past its start, so that B and C can
+    be handed over with 4- or 8-byte alignment only."""
+
+    def __init__(self, vs, a, off, st):
+        import ctypes
+        self._lib = vs.load_library()
+        self._st = st
+        self.shape, self.nbytes = a.shape, a.nbytes
+        self._base = vs.DeviceArray((a.nbytes + 64,), np.uint8)
+        self.ptr = ctypes.c_void_p(self._base.ptr.value + off)
+        a = np.ascontiguousarray(a)
+        assert self._lib.vcsr_memcpy_h2d(self.ptr, a.ctypes.data_as(ctypes.c_void_p), a.nbytes,
+                                         st.h) == 0
+        st.sync()
+
+    def numpy(self):
+        import ctypes
+        out = np.empty(self.shape, np.float32)
+        assert self._lib.vcsr_memcpy_d2h(out.ctypes.data_as(ctypes.c_void_p), self.ptr,
+                                         self.nbytes, self._st.h) == 0
+        self._st.sync()
+        return out
+
+
+@pytest.mark.parametrize("off", [4, 8])
+@pytest.mark.parametrize("kind", ["tile3", "tile16", "tile1", "row", "wave"])
+def test_unaligned_b_and_c(gpu, orc, st, kind, off):
+    """B and C that are only 4- or 8-byte aligned take the narrower per-lane
+    vectors (1 or 2 floats) of the row, tile and wave kernels."""
+    vs = gpu
+    rng = np.random.default_rng(off)
+    O = 128
+    csr = _block_csr(vs, rng, 24, 3, 400, 8, 3, 0.8)
+    B = vs.gen_dense(off, 0, csr.N, O)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    dB = _Shifted(vs, B, off, st)
+    dC = _Shifted(vs, np.full((csr.M, O), 9.0, np.float32), off, st)
+    if kind == "wave":
+        rp, col, val = _device_csr(vs, csr, st)
+        vs.run_csr_wave_spmm_gpu(csr.M, csr.N, rp, col, val, dB, O, dC, st, timed=True)
+    else:
+        fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+        if kind.startswith("tile"):
+            fmt.set_tile_rows(int(kind[4:]))
+        fmt.upload(st)
+        kernel = vs.KERNEL_ROW if kind == "row" else vs.KERNEL_TILE
+        vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, 64, dC, st, timed=True, kernel=kernel,
+                                accumulate=False)
+    assert_within_tolerance(dC.numpy(), ref64, csr.row_ptr, csr.val, B, f"{kind} off{off}")
