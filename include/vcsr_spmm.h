@@ -131,6 +131,15 @@ typedef struct {
 int vcsr_build(const vcsr_csr* csr, int32_t segw, int32_t bundle,
                int32_t layout, int32_t nthreads, vcsr_fmt** out);
 int vcsr_fmt_arrays(const vcsr_fmt* fmt, vcsr_arrays* out);
+/* Write a built format (its host arrays and the row-tile view settings of
+ * vcsr_fmt_set_tile_rows / _windows) to a file, and read one back as a new
+ * handle that is bit-identical to the saved one and not uploaded, so a
+ * matrix's format is built once (the reference rebuilds it every run,
+ * src/main.cpp:128-149).  A file that cannot be read is VCSR_EIO; one whose
+ * contents break the format's invariants (array sizes, group pointers,
+ * rows, columns, segment table) is VCSR_EINVAL.  No reference counterpart. */
+int vcsr_fmt_save(const vcsr_fmt* fmt, const char* path);
+int vcsr_fmt_load(const char* path, vcsr_fmt** out);
 /* Copy the format to the current device (once; later calls are no-ops).
  * Replaces the per-call cudaMallocAsync/cudaMemcpyAsync of
  * src/kernels.cu:139-151 and the one-time static upload of

@@ -569,3 +569,26 @@ def test_unaligned_b_and_c(gpu, orc, st, kind, off):
         vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, 64, dC, st, timed=True, kernel=kernel,
                                 accumulate=False)
     assert_within_tolerance(dC.numpy(), ref64, csr.row_ptr, csr.val, B, f"{kind} off{off}")
+
+
+def test_loaded_format_computes_the_same(gpu, orc, st, tmp_path):
+    """A format saved and loaded back (with its tile settings) uploads and
+    gives bit-identical results to the format it was saved from."""
+    vs = gpu
+    rng = np.random.default_rng(3)
+    csr = _block_csr(vs, rng, 30, 16, 500, 6, 16, 0.9)
+    O = 96
+    B = vs.gen_dense(5, 0, csr.N, O)
+    fmt = vs.build_vcsr(csr, 16, 16, vs.LAYOUT_TC)
+    fmt.set_tile_rows(16)
+    path = str(tmp_path / "f.vcsr")
+    vs.save_vcsr(fmt, path)
+    back = vs.load_vcsr(path)
+    outs = []
+    for f in (fmt, back):
+        f.upload(st)
+        assert f.tile_info()[0] == 16
+        outs.append(_ex(vs, f, B, np.zeros((csr.M, O), np.float32), st, vs.KERNEL_TILE, False))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert_within_tolerance(outs[1], ref64, csr.row_ptr, csr.val, B, "loaded")

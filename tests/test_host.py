@@ -294,3 +294,84 @@ def test_mfma_work_counts_padding(vs):
     assert fpo == 2 * 32 * 32 * 2
     assert ops == sum(-(-n // 32) for n in nact) * 2 * 4
     assert ops * fpo >= 2 * csr.nnz * O
+
+
+@pytest.mark.parametrize("layout,segw,bundle", [(0, 4, 32), (1, 4, 64), (1, 3, 7), (2, 16, 16)])
+def test_format_file_round_trip(vs, tmp_path, layout, segw, bundle):
+    """A saved format loads back with bit-identical arrays and the same
+    parameters (a matrix with empty rows, duplicates and ragged rows)."""
+    rng = np.random.default_rng(layout * 10 + segw)
+    M, N = 200, 150
+    rows = rng.integers(0, M, 1500).astype(np.int32)
+    rows[rows % 9 == 0] = 3  # one long row, some empty ones
+    cols = rng.integers(0, N, 1500).astype(np.int32)
+    vals = rng.uniform(-1, 1, 1500).astype(np.float32)
+    csr = vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
+    fmt = vs.build_vcsr(csr, segw, bundle, layout)
+    fmt.set_tile_rows(16)
+    fmt.set_tile_windows(True)
+    path = str(tmp_path / "a.vcsr")
+    vs.save_vcsr(fmt, path)
+    back = vs.load_vcsr(path)
+    a, b = fmt.arrays(), back.arrays()
+    assert a.keys() == b.keys()
+    for k in a:
+        assert np.array_equal(a[k].view(np.uint32) if a[k].dtype == np.float32 else a[k],
+                              b[k].view(np.uint32) if b[k].dtype == np.float32 else b[k]), k
+    for attr in ("num_groups", "num_slots"):
+        assert getattr(fmt, attr) == getattr(back, attr)
+    # The tile-view settings travel with the file: a second save is identical.
+    path2 = str(tmp_path / "b.vcsr")
+    vs.save_vcsr(back, path2)
+    assert open(path, "rb").read() == open(path2, "rb").read()
+
+
+def test_format_file_rejects_bad_files(vs, tmp_path):
+    """Unreadable files are VCSR_EIO; files whose header or arrays break the
+    format's invariants are VCSR_EINVAL (never a handle the kernels could
+    index out of bounds with)."""
+    csr = vs.coo_to_csr(vs.generate_coo(1, 0))
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    good = tmp_path / "good.vcsr"
+    vs.save_vcsr(fmt, str(good))
+    data = bytearray(good.read_bytes())
+    G = fmt.num_groups
+
+    def expect(blob, code, name):
+        p = tmp_path / name
+        p.write_bytes(bytes(blob))
+        with pytest.raises(vs.VcsrError) as e:
+            vs.load_vcsr(str(p))
+        assert e.value.code == code, (name, e.value)
+
+    with pytest.raises(vs.VcsrError) as e:
+        vs.load_vcsr(str(tmp_path / "missing.vcsr"))
+    assert e.value.code == vs.VCSR_EIO
+    expect(data[:20], vs.VCSR_EIO, "short_header")
+    bad = bytearray(data); bad[0:8] = b"NOTVCSR!"
+    expect(bad, vs.VCSR_EINVAL, "magic")
+    expect(data[:-4], vs.VCSR_EINVAL, "truncated")
+    expect(data + bytes(4), vs.VCSR_EINVAL, "trailing")
+    hdr = 8 + 32 + 16  # magic, 8 int32, 2 int64
+    ptr0 = hdr                        # group_ptr
+    depth0 = ptr0 + 4 * (G + 1)       # group_depth
+    base0 = depth0 + 4 * G            # group_seg_base
+    rows0 = base0 + 4 * G             # group_rows
+    lcol0 = rows0 + 4 * G * 64        # lcol
+    def with_int(off, value, name):
+        b = bytearray(data)
+        b[off:off + 4] = np.int32(value).tobytes()
+        expect(b, vs.VCSR_EINVAL, name)
+    with_int(8 + 8, 0, "bundle_zero")             # bundle field of the header
+    with_int(8 + 4, 10 ** 6, "n_mismatch")        # N no longer matches segments
+    with_int(ptr0 + 4, 7, "group_ptr")            # group 0 no longer depth * bundle
+    with_int(depth0, -1, "negative_depth")
+    with_int(base0, 4, "segment_base")            # group 0 sits in segment 0
+    with_int(rows0, csr.M, "row_out_of_range")
+    with_int(lcol0, 4, "lcol_out_of_segment")     # segw = 4
+    # An entry after a padding slot of the same lane.
+    a = fmt.arrays()
+    pad = int(np.nonzero(a["lcol"] < 0)[0][0])
+    with_int(lcol0 + 4 * pad, 0, "unpacked_lane")
+    # The untouched file still loads.
+    assert vs.load_vcsr(str(good)).num_groups == G

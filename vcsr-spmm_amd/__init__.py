@@ -40,7 +40,8 @@ KERNEL_AUTO, KERNEL_SEGMENT, KERNEL_MFMA, KERNEL_ROW, KERNEL_TILE = 0, 1, 2, 3, 
 EXPORTS = (
     "vcsr_last_error vcsr_version vcsr_mtx_read vcsr_coo_create vcsr_coo_view_get "
     "vcsr_coo_free vcsr_gen_coo vcsr_gen_dense vcsr_coo_to_csr vcsr_csr_create "
-    "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_upload "
+    "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_save vcsr_fmt_load "
+    "vcsr_fmt_upload "
     "vcsr_fmt_set_tile_rows vcsr_fmt_set_tile_windows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_csr_wave spmm_vcsr "
     "spmm_vcsr_ex spmm_vcsr_mfma vcsr_mfma_work vcsr_tile_mfma_work spmm_csr_cpu "
     "vcsr_vendor_plan_create vcsr_vendor_spmm vcsr_vendor_plan_free spmm_csr_vendor "
@@ -108,6 +109,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "vcsr_build": (C.c_int, [P, I32, I32, I32, I32, pP]),
         "vcsr_fmt_arrays": (C.c_int, [P, C.POINTER(_Arrays)]),
         "vcsr_fmt_upload": (C.c_int, [P, P]),
+        "vcsr_fmt_save": (C.c_int, [P, C.c_char_p]),
+        "vcsr_fmt_load": (C.c_int, [C.c_char_p, pP]),
         "vcsr_fmt_set_tile_rows": (C.c_int, [P, I32]),
         "vcsr_fmt_set_tile_windows": (C.c_int, [P, I32]),
         "vcsr_fmt_tile_info": (C.c_int, [P, pI, C.POINTER(I64), C.POINTER(I64)]),
@@ -300,6 +303,18 @@ class Vcsr:
         r, t, e = C.c_int32(), C.c_int64(), C.c_int64()
         _check(load_library().vcsr_fmt_tile_info(self._h, C.byref(r), C.byref(t), C.byref(e)))
         return r.value, t.value, e.value
+
+
+def save_vcsr(fmt: "Vcsr", path: str) -> None:
+    """Write the format (host arrays, tile-view settings) to a file."""
+    _check(load_library().vcsr_fmt_save(fmt._h, os.fsencode(path)))
+
+
+def load_vcsr(path: str) -> "Vcsr":
+    """Read a format file written by save_vcsr (validated; not uploaded)."""
+    h = C.c_void_p()
+    _check(load_library().vcsr_fmt_load(os.fsencode(path), C.byref(h)))
+    return Vcsr(h)
 
 
 def build_vcsr(csr: Csr, segw: int, bundle: int, layout: int, nthreads: int = 0) -> Vcsr:

@@ -2,11 +2,13 @@
 // Each wrapper catches every exception and turns it into a status code plus
 // a thread-local message; no exception crosses the C ABI.
 #include <cstring>
+#include <memory>
 #include <new>
 #include <string>
 
 #include "../../include/vcsr_spmm.h"
 #include "fmt_internal.hpp"
+#include "host/fmt_io.hpp"
 
 namespace vcsr {
 namespace {
@@ -205,6 +207,23 @@ int vcsr_fmt_arrays(const vcsr_fmt* fmt, vcsr_arrays* out) {
         out->lcol = v.lcol.data();
         out->val = v.val.data();
         out->segment_group_start = v.segment_group_start.data();
+    });
+}
+
+int vcsr_fmt_save(const vcsr_fmt* fmt, const char* path) {
+    return guarded([&] {
+        need(fmt && path, "null argument");
+        vcsr::save_vcsr(fmt->v, fmt->tile_rows, fmt->tile_fixed, path);
+    });
+}
+
+int vcsr_fmt_load(const char* path, vcsr_fmt** out) {
+    return guarded([&] {
+        need(path && out, "null argument");
+        *out = nullptr;
+        std::unique_ptr<vcsr_fmt> f(new vcsr_fmt());
+        f->v = vcsr::load_vcsr(path, &f->tile_rows, &f->tile_fixed);
+        *out = f.release();
     });
 }
 
