@@ -107,3 +107,28 @@ def test_cli_gpu_algo_without_gpu(vs):
         pytest.skip("a GPU is visible")
     r = run_cli(vs, "--gen", "cfg1", "--algo", "vcsr")
     assert r.returncode == 2 and "no GPU" in r.stderr
+
+
+@pytest.mark.gpu
+def test_cli_gpu_algorithms_and_format_file(vs, tmp_path):
+    """On the GPU: every algorithm's result line parses like the reference's
+    bench scripts read it (number before "ms" and before "GFLOP/s"), the L2
+    check passes, and --save-fmt / --load-fmt round-trip the VCSR format."""
+    if vs.device_count() <= 0:
+        pytest.fail("no GPU visible to the library (gpu tests run on the GPU box)")
+    fmt = str(tmp_path / "cfg1.vcsr")
+    for algo, extra in (("vcsr", ["--save-fmt", fmt]), ("vcsr", ["--load-fmt", fmt]),
+                        ("csr", []), ("vcsr_mfma", []), ("vcsr_tc", []), ("rocsparse", []),
+                        ("aspt", []), ("fast", [])):
+        r = run_cli(vs, "--gen", "cfg1", "--O", "64", "--algo", algo, "--repeat", "2",
+                    "--check", *extra)
+        assert r.returncode == 0, (algo, r.stdout[-2000:], r.stderr[-2000:])
+        last = r.stdout.strip().splitlines()[-1].split()
+        ms = float(last[last.index("ms") - 1])
+        gf = float(last[last.index("GFLOP/s") - 1])
+        assert ms > 0 and gf > 0, (algo, last)
+        assert "FAIL" not in r.stdout, (algo, r.stdout[-2000:])
+        if "--save-fmt" in extra:
+            assert "format: saved to" in r.stdout
+        if "--load-fmt" in extra:
+            assert "format: loaded from" in r.stdout

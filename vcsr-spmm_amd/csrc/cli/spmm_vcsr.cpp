@@ -46,12 +46,15 @@ struct Opts {
     bool check = false;
     bool expand = false;
     int threads = 0;
+    std::string save_fmt, load_fmt;  // VCSR format file for --algo vcsr
 };
 
 void usage() {
     std::printf("Usage: spmm_vcsr (--mtx file.mtx | --gen cfgN) --O 128 [options]\n");
     std::printf("Options: --segw w --bundle b --tileK t --repeat r --warmup w --seed s\n");
     std::printf("         --layout H|S --check --threads T --expand-symmetric\n");
+    std::printf("         --save-fmt F (write the built VCSR format) --load-fmt F (use it\n");
+    std::printf("         instead of building; --algo vcsr)\n");
     std::printf("Algorithms: csr, vcsr (vcsr_baseline, vcsr_seg), vcsr_mfma, vcsr_tc, "
                 "rocsparse (cusparse), aspt, fast (fastspmm), cpu, all\n");
 }
@@ -114,6 +117,7 @@ int main(int argc, char** argv) {
         {"seed", required_argument, 0, 'S'},   {"layout", required_argument, 0, 'L'},
         {"warmup", required_argument, 0, 'w'}, {"check", no_argument, 0, 'c'},
         {"threads", required_argument, 0, 'T'}, {"expand-symmetric", no_argument, 0, 'e'},
+        {"save-fmt", required_argument, 0, 'F'}, {"load-fmt", required_argument, 0, 'l'},
         {"help", no_argument, 0, 'h'},         {0, 0, 0, 0}};
     int copt, idx;
     while ((copt = getopt_long(argc, argv, "", long_opts, &idx)) != -1) {
@@ -137,6 +141,8 @@ int main(int argc, char** argv) {
             case 'c': o.check = true; break;
             case 'T': o.threads = std::atoi(optarg); break;
             case 'e': o.expand = true; break;
+            case 'F': o.save_fmt = optarg; break;
+            case 'l': o.load_fmt = optarg; break;
             case 'h': usage(); return 0;
             default: usage(); return 1;
         }
@@ -305,7 +311,24 @@ int main(int argc, char** argv) {
         const bool mfma = kind == 1;
         vcsr_fmt* fmt = nullptr;
         const double t0 = now_ms();
-        CHECK(vcsr_build(csr, segw, bundle, lay, o.threads, &fmt));
+        const bool from_file = kind == 0 && !o.load_fmt.empty();
+        if (from_file) {
+            CHECK(vcsr_fmt_load(o.load_fmt.c_str(), &fmt));
+            vcsr_arrays la;
+            CHECK(vcsr_fmt_arrays(fmt, &la));
+            if (la.M != A.M || la.N != A.N) {
+                std::fprintf(stderr, "spmm_vcsr: %s holds a %d x %d format, the matrix is %d x %d\n",
+                             o.load_fmt.c_str(), la.M, la.N, A.M, A.N);
+                std::exit(1);
+            }
+            std::printf("format: loaded from %s\n", o.load_fmt.c_str());
+        } else {
+            CHECK(vcsr_build(csr, segw, bundle, lay, o.threads, &fmt));
+        }
+        if (kind == 0 && !o.save_fmt.empty()) {
+            CHECK(vcsr_fmt_save(fmt, o.save_fmt.c_str()));
+            std::printf("format: saved to %s\n", o.save_fmt.c_str());
+        }
         if (kind == 2) {
             CHECK(vcsr_fmt_set_tile_rows(fmt, 16));
             CHECK(vcsr_fmt_set_tile_windows(fmt, 1));
