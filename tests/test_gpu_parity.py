@@ -592,3 +592,30 @@ def test_loaded_format_computes_the_same(gpu, orc, st, tmp_path):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
     assert_within_tolerance(outs[1], ref64, csr.row_ptr, csr.val, B, "loaded")
+
+
+@pytest.mark.parametrize("fixed", [False, True])
+@pytest.mark.parametrize("O", [16, 100, 512])
+def test_mfma_tiles_are_bit_exact(gpu, orc, st, fixed, O):
+    """v_mfma_f32_16x16x4f32 adds its four products to the accumulator one
+    after the other with one rounding each, and the tile kernel feeds each
+    row's entries in column order, so 16-row tiles that are not split into
+    pieces reproduce the oracle's FP32 loop (one fused multiply-add per term
+    in CSR order) bit for bit: dense and partly filled 16x16 blocks, and
+    fixed windows over a matrix without block structure."""
+    vs = gpu
+    rng = np.random.default_rng(O + (7 if fixed else 0))
+    if fixed:
+        csr = _case(vs, orc, rng, 320, 400, density=0.05, dup_rate=0.0, empty_rows=0.1)
+    else:
+        csr = _block_csr(vs, rng, 20, 16, 640, 12, 16, 0.85)
+    B = vs.gen_dense(O + 3, 1, csr.N, O)
+    fmt = vs.build_vcsr(csr, 16, 16, vs.LAYOUT_TC)
+    fmt.set_tile_rows(16)
+    fmt.set_tile_windows(fixed)
+    fmt.upload(st)
+    R, tiles, entries = fmt.tile_info()
+    assert R == 16 and entries <= tiles * 1024  # no tile is split
+    got = _ex(vs, fmt, B, np.zeros((csr.M, O), np.float32), st, vs.KERNEL_TILE, False)
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
