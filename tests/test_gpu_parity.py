@@ -302,7 +302,7 @@ def _block_csr(vs, rng, nbr, bh, N, blocks_per_row, bw, keep):
 @pytest.mark.parametrize("bh,tile_rows", [(2, 0), (3, 0), (4, 0), (8, 0), (16, 0), (3, 1), (3, 2),
                                           (3, 3), (6, 3), (3, 8), (5, 4), (16, 16), (5, 16),
                                           (12, 16)])
-@pytest.mark.parametrize("O", [1, 8, 33, 128, 200, 520])
+@pytest.mark.parametrize("O", [1, 8, 33, 128, 200, 520, 2048])
 def test_tile_kernel_block_rows(gpu, orc, st, bh, tile_rows, O):
     vs = gpu
     rng = np.random.default_rng(bh * 100 + tile_rows * 10 + O)
