@@ -619,3 +619,52 @@ def test_mfma_tiles_are_bit_exact(gpu, orc, st, fixed, O):
     got = _ex(vs, fmt, B, np.zeros((csr.M, O), np.float32), st, vs.KERNEL_TILE, False)
     ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as hst
+
+
+@settings(max_examples=40, deadline=None,
+          suppress_health_check=[HealthCheck.function_scoped_fixture, HealthCheck.too_slow])
+@given(M=hst.integers(1, 300), N=hst.integers(1, 300), bh=hst.sampled_from([1, 2, 3, 4, 8, 16]),
+       keep=hst.floats(0.3, 1.0), tile_rows=hst.sampled_from([0, 1, 2, 3, 4, 8, 16]),
+       fixed=hst.booleans(), O=hst.sampled_from([1, 3, 8, 16, 31, 64, 100, 128, 257]),
+       accumulate=hst.booleans(), seed=hst.integers(0, 2 ** 31 - 1))
+def test_tile_kernel_property(gpu, orc, st, M, N, bh, keep, tile_rows, fixed, O, accumulate,
+                              seed):
+    """Random shapes, block heights, densities, tile heights (automatic,
+    forced, fixed windows), widths and accumulate modes: the tile kernel
+    (VALU and MFMA paths) agrees with the oracle within the north-star
+    tolerance."""
+    vs = gpu
+    rng = np.random.default_rng(seed)
+    nbr = -(-M // bh)
+    rows, cols = [], []
+    for br in range(nbr):
+        for c0 in rng.choice(max(1, N), size=min(N, int(rng.integers(0, 6))), replace=False):
+            rr, cc = np.meshgrid(np.arange(bh) + br * bh, np.arange(min(3, N - c0)) + c0,
+                                 indexing="ij")
+            m = (rng.random(rr.shape) < keep) & (rr < M)
+            rows.append(rr[m]); cols.append(cc[m])
+    rows = np.concatenate(rows).astype(np.int32) if rows else np.zeros(0, np.int32)
+    cols = np.concatenate(cols).astype(np.int32) if cols else np.zeros(0, np.int32)
+    key = np.unique(rows.astype(np.int64) * N + cols)
+    rows, cols = (key // N).astype(np.int32), (key % N).astype(np.int32)
+    vals = rng.uniform(-1, 1, rows.size).astype(np.float32)
+    csr = vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
+    B = vs.gen_dense(int(seed % 1000), 0, N, O)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.set_tile_rows(tile_rows)
+    fmt.set_tile_windows(fixed and tile_rows > 0)
+    fmt.upload(st)
+    C0 = rng.uniform(-1, 1, size=(M, O)).astype(np.float32)
+    got = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate)
+    if accumulate:
+        got = got - C0
+    ref64 = orc.spmm_f64(M, csr.row_ptr, csr.col, csr.val, B)
+    if csr.nnz:
+        assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B,
+                                f"M{M} N{N} bh{bh} R{tile_rows} fixed{fixed} O{O}")
+    else:
+        assert np.abs(got).max(initial=0.0) <= 1e-6
