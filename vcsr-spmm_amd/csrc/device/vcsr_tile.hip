@@ -81,13 +81,15 @@ __device__ __forceinline__ void load_vals(const float* p, float (&a)[R]) {
     }
 }
 
-__device__ __forceinline__ bool all_finite(float x) { return __builtin_isfinite(x); }
-__device__ __forceinline__ bool all_finite(float2 x) {
-    return __builtin_isfinite(x.x) && __builtin_isfinite(x.y);
+// z + x * 0 for every component of x, as fused multiply-adds (no rounding:
+// x * 0 is a signed zero for finite x, NaN otherwise).
+__device__ __forceinline__ float fma_zero_acc(float x, float z) { return __builtin_fmaf(x, 0.f, z); }
+__device__ __forceinline__ float fma_zero_acc(float2 x, float z) {
+    return __builtin_fmaf(x.y, 0.f, __builtin_fmaf(x.x, 0.f, z));
 }
-__device__ __forceinline__ bool all_finite(float4 x) {
-    return __builtin_isfinite(x.x) && __builtin_isfinite(x.y) && __builtin_isfinite(x.z) &&
-           __builtin_isfinite(x.w);
+__device__ __forceinline__ float fma_zero_acc(float4 x, float z) {
+    return __builtin_fmaf(x.w, 0.f, __builtin_fmaf(x.z, 0.f, __builtin_fmaf(x.y, 0.f,
+                          __builtin_fmaf(x.x, 0.f, z))));
 }
 
 // One wave per MERGE consecutive work items of the view.  BUF: B smaller than
@@ -110,10 +112,13 @@ void vcsr_tile_kernel(
     constexpr int EMAX = tile_piece_entries(R) * MERGE;      // entries per wave
     constexpr int PMAX = kTileChunkPieces * MERGE;           // pieces per wave
     constexpr int U = 8;                                     // loads per block
-    __shared__ uint32_t s_brow[kWaves][EMAX];
-    __shared__ uint8_t s_mask[kWaves][EMAX];
+    // A one-piece item's list is padded with "no row" entries of value 0 up
+    // to a multiple of S*U, so that all its blocks are full blocks.
+    constexpr int EPAD = (EMAX + S * U - 1) / (S * U) * (S * U);
+    __shared__ uint32_t s_brow[kWaves][EPAD];
+    __shared__ uint8_t s_mask[kWaves][EPAD];
     __shared__ uint8_t s_bad[kWaves][PMAX];
-    __shared__ __align__(16) float s_val[kWaves][EMAX * RS];
+    __shared__ __align__(16) float s_val[kWaves][EPAD * RS];
     __shared__ int4 s_piece[kWaves][PMAX + 2];
     __shared__ int32_t s_first[kWaves][S + 1];
 
@@ -133,14 +138,23 @@ void vcsr_tile_kernel(
     const int32_t e0 = uniform(chunks[c0].x), ne = uniform(chunks[c1].y) - e0;  // <= EMAX
     const int32_t p0 = uniform(chunks[c0].z), np = uniform(chunks[c1].w) - p0;  // <= PMAX
 
-    // Phase 1: stage the entries and the piece table.
+    // Phase 1: stage the entries (and a one-piece item's padding, buffer
+    // path) and the piece table.
     const uint32_t row_bytes = (uint32_t)O * 4u;
-    for (int32_t i = lane; i < ne; i += 64) {
-        const int64_t e = (int64_t)e0 + i;
-        const uint32_t br = (uint32_t)ent_brow[e];
-        const uint32_t m = ent_mask[e];
+    const bool pad = BUF && np == 1;
+    const int32_t ne_pad = pad ? (ne + S * U - 1) / (S * U) * (S * U) : ne;  // <= EPAD
+    for (int32_t i = lane; i < ne_pad; i += 64) {
+        uint32_t br = 0, m = 0;
         float a[RS];
-        load_vals<RS>(ent_val + e * RS, a);
+        if (i < ne) {
+            const int64_t e = (int64_t)e0 + i;
+            br = (uint32_t)ent_brow[e];
+            m = ent_mask[e];
+            load_vals<RS>(ent_val + e * RS, a);
+        } else {
+#pragma unroll
+            for (int q = 0; q < RS; ++q) a[q] = 0.f;
+        }
         lb[i] = BUF ? (m ? br * row_bytes : kNoRow) : br;
         lm[i] = (uint8_t)m;
         store_vals<RS>(lv + i * RS, a);
@@ -183,14 +197,16 @@ void vcsr_tile_kernel(
 #pragma unroll
         for (int r = 0; r < R; ++r) fma_vec(acc[r], ok ? a[r] : 0.f, b);
     };
-    // Whether every value this lane would write for piece pidx is finite.
-    auto piece_finite = [&](int32_t pidx, const V (&acc)[R], bool kok) -> bool {
-        const int32_t rows = lp[pidx].y;
-        bool fin = true;
+    // Whether every accumulator of this lane is finite (lanes past O hold
+    // nothing to store).  z = fma(x, 0, z) over all of them stays finite
+    // exactly when every x is (x * 0 is NaN for inf and NaN).  Rows absent
+    // from the piece are included: their sums are zero for finite B, so this
+    // can only send a piece to the exact recomputation more often.
+    auto piece_finite = [&](const V (&acc)[R], bool kok) -> bool {
+        float z = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (r < rows) fin = fin && all_finite(acc[r]);
-        return fin || !kok;
+        for (int r = 0; r < R; ++r) z = fma_zero_acc(acc[r], z);
+        return __builtin_isfinite(z) || !kok;
     };
     // Writes the accumulated rows of piece pidx (its first pc.y rows exist)
     // to C or to its partial rows.
@@ -280,7 +296,7 @@ void vcsr_tile_kernel(
                         // A stream stores a piece only if all its lanes' sums
                         // are finite; otherwise redo_piece computes and stores
                         // it after the loop.
-                        const uint64_t bm = __ballot(!piece_finite(p, acc, kok));
+                        const uint64_t bm = __ballot(!piece_finite(acc, kok));
                         if ((bm & smask) != 0) {
                             bad = true;
                             lbad[p] = 1;
@@ -333,9 +349,13 @@ void vcsr_tile_kernel(
                     apply(acc, ok ? t : 0, ok, b[u]);
                 }
             };
-            for (int32_t i0 = 0; i0 < nper; i0 += U) {
-                if (i0 + U <= nfull) block(std::true_type(), i0);
-                else block(std::false_type(), i0);
+            if constexpr (BUF) {
+                for (int32_t i0 = 0; i0 < ne_pad / S; i0 += U) block(std::true_type(), i0);
+            } else {
+                for (int32_t i0 = 0; i0 < nper; i0 += U) {
+                    if (i0 + U <= nfull) block(std::true_type(), i0);
+                    else block(std::false_type(), i0);
+                }
             }
 #pragma unroll
             for (int sh = LPE; sh < 64; sh <<= 1) {
@@ -344,7 +364,7 @@ void vcsr_tile_kernel(
             }
             // Stream 0 stores the sum, or recomputes it exactly when any of
             // its lanes' values is not finite.
-            const bool bad = sub == 0 && !piece_finite(0, acc, kok);
+            const bool bad = sub == 0 && !piece_finite(acc, kok);
             if (__any(bad)) {
                 if (sub == 0) redo_piece(0, k, koff, kok);
             } else if (sub == 0) {
