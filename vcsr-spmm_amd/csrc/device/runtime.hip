@@ -160,6 +160,12 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
         std::vector<int32_t> items = make_items(v, 256);
         RowView rv = make_row_view(v, nact);
         const vcsr::TileView tv = vcsr::make_tile_view(v, fmt->tile_rows, 0, fmt->tile_fixed);
+        // Device copy of the entries' B rows: placeholders (no row present)
+        // are marked kTileNoEntry, so the kernels tell them apart without
+        // reading the presence bits.
+        std::vector<int32_t> tv_brow(tv.brow);
+        for (size_t q = 0; q < tv_brow.size(); ++q)
+            if (tv.mask[q] == 0) tv_brow[q] = vcsr::kTileNoEntry;
         DeviceFmt d;
         hip_check(hipGetDevice(&d.device), "hipGetDevice");
         try {
@@ -185,7 +191,7 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.tv_chunks = upload_array(tv.chunks, st, "upload tile chunks");
             d.tv_n_chunks = (int32_t)(tv.chunks.size() / 4);
             d.tv_pieces = upload_array(tv.pieces, st, "upload tile pieces");
-            d.tv_brow = upload_array(tv.brow, st, "upload tile entries");
+            d.tv_brow = upload_array(tv_brow, st, "upload tile entries");
             d.tv_val = upload_array(tv.val, st, "upload tile values");
             d.tv_mask = upload_array(tv.mask, st, "upload tile masks");
             d.tv_n_entries = tv.n_entries();

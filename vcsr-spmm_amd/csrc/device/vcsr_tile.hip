@@ -116,7 +116,6 @@ void vcsr_tile_kernel(
     // to a multiple of S*U, so that all its blocks are full blocks.
     constexpr int EPAD = (EMAX + S * U - 1) / (S * U) * (S * U);
     __shared__ uint32_t s_brow[kWaves][EPAD];
-    __shared__ uint8_t s_mask[kWaves][EPAD];
     __shared__ uint8_t s_bad[kWaves][PMAX];
     __shared__ __align__(16) float s_val[kWaves][EPAD * RS];
     __shared__ int4 s_piece[kWaves][PMAX + 2];
@@ -130,7 +129,6 @@ void vcsr_tile_kernel(
     if (c0 >= n_chunks) return;
     const int32_t c1 = min(n_chunks, c0 + MERGE) - 1;
     uint32_t* lb = s_brow[wave];
-    uint8_t* lm = s_mask[wave];
     uint8_t* lbad = s_bad[wave];
     float* lv = s_val[wave];
     int4* lp = s_piece[wave];
@@ -144,19 +142,19 @@ void vcsr_tile_kernel(
     const bool pad = BUF && np == 1;
     const int32_t ne_pad = pad ? (ne + S * U - 1) / (S * U) * (S * U) : ne;  // <= EPAD
     for (int32_t i = lane; i < ne_pad; i += 64) {
-        uint32_t br = 0, m = 0;
+        uint32_t br = (uint32_t)kTileNoEntry;
         float a[RS];
         if (i < ne) {
             const int64_t e = (int64_t)e0 + i;
             br = (uint32_t)ent_brow[e];
-            m = ent_mask[e];
             load_vals<RS>(ent_val + e * RS, a);
         } else {
 #pragma unroll
             for (int q = 0; q < RS; ++q) a[q] = 0.f;
         }
-        lb[i] = BUF ? (m ? br * row_bytes : kNoRow) : br;
-        lm[i] = (uint8_t)m;
+        // Placeholders: "no row" on the buffer path, else row 0 times 0.
+        const bool real = br != (uint32_t)kTileNoEntry;
+        lb[i] = BUF ? (real ? br * row_bytes : kNoRow) : (real ? br : 0u);
         store_vals<RS>(lv + i * RS, a);
     }
     for (int32_t j = lane; j < np; j += 64) {
@@ -234,7 +232,7 @@ void vcsr_tile_kernel(
             const V b = load_b(t, true, koff);
             float a[RS];
             load_vals<RS>(lv + t * RS, a);
-            const uint32_t m = lm[t];
+            const uint32_t m = ent_mask[(int64_t)e0 + t];
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if ((m >> r) & 1u) fma_vec(acc[r], a[r], b);
@@ -478,7 +476,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
     const uint32_t row_bytes = (uint32_t)O * 4u;
     for (int32_t i = lane; i < ne; i += 64) {
         const uint32_t br = (uint32_t)ent_brow[e0 + i];
-        const bool any = ent_mask[e0 + i] != 0;
+        const bool any = br != (uint32_t)kTileNoEntry;
         lb[i] = BUF ? (any ? br * row_bytes : kNoRow) : (any ? br : kNoRow);
     }
     wave_sync();

@@ -61,6 +61,9 @@ constexpr int64_t tile_val_index(int32_t R, int64_t e, int32_t r) {
 }
 // Tile pieces per work item.
 constexpr int32_t kTileChunkPieces = 32;
+// B row of a placeholder entry (no tile row present) in the device copy of
+// the view's B-row array; the host view keeps 0 there.
+constexpr int32_t kTileNoEntry = -1;
 // Rows are cut into tiles inside fixed blocks of this many rows (so that
 // blocks can be tiled in parallel and the view never depends on the thread
 // count).
