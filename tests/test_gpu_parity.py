@@ -389,6 +389,41 @@ def test_b_of_2gb_or_more_uses_64bit_addresses(gpu, orc, st, kind, tile_rows):
     _rowsample_check(vs, orc, csr, B, C, 300, 21)
 
 
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_tile_column_slices_with_split_rows(gpu, orc, st, accumulate):
+    """B larger than 512 MB at O > 128 runs in column slices of 128 columns
+    (one launch per slice, B and C rows O floats apart); rows too long for
+    one work item are cut into pieces whose partial sums the reduce kernel
+    adds, slice by slice.  N = 700,000, O = 200 (560 MB; slices of 128 and
+    72 columns), 2,000 rows of which every 50th has 3,000 entries, the
+    others 12; columns uniform over N, so the view keeps 1-row tiles."""
+    vs = gpu
+    rng = np.random.default_rng(5)
+    N, O, M = 700_000, 200, 2000
+    lens = np.where(np.arange(M) % 50 == 7, 3000, 12)
+    rows = np.repeat(np.arange(M, dtype=np.int32), lens)
+    cols = rng.integers(0, N, size=rows.size).astype(np.int32)
+    vals = rng.uniform(-1, 1, size=rows.size).astype(np.float32)
+    csr = vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
+    B = vs.gen_dense(9, 0, N, O)
+    assert B.nbytes > 512 << 20
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.upload(st)
+    assert fmt.tile_info()[0] == 1
+    C0 = rng.uniform(-1, 1, size=(M, O)).astype(np.float32)
+    C = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate)
+    if accumulate:
+        C = C - C0
+    sample = np.unique(np.concatenate([np.nonzero(lens > 100)[0],
+                                       rng.choice(M, size=200, replace=False)]))
+    n = np.diff(csr.row_ptr)[sample]
+    rp = np.concatenate([[0], np.cumsum(n)]).astype(np.int32)
+    sc = np.concatenate([csr.col[csr.row_ptr[r]:csr.row_ptr[r + 1]] for r in sample])
+    sv = np.concatenate([csr.val[csr.row_ptr[r]:csr.row_ptr[r + 1]] for r in sample])
+    ref64 = orc.spmm_f64(len(sample), rp, sc, sv, B)
+    assert_within_tolerance(C[sample], ref64, rp, sv, B, "sliced rows")
+
+
 @pytest.mark.parametrize("O", [8, 32, 100, 512])
 def test_tile_mfma_work_counts_the_launch(gpu, orc, st, O):
     """The MFMA instruction count of 16-row tiles: four entries per k-step,

@@ -33,6 +33,7 @@
 // select); this is exact for finite B.  A piece whose sum comes out
 // non-finite is recomputed with the presence bits before it is stored, so
 // inf / NaN in B reach exactly the rows the reference's loop reaches.
+#include <algorithm>
 #include <type_traits>
 
 #include "../host/tile_view.hpp"
@@ -47,6 +48,9 @@ constexpr int kWaves = 4;
 // Buffer offset of "no B row": at least 2^31, above any buffer-path B size,
 // and still below 2^32 after adding a column offset (< 2^31).
 constexpr uint32_t kNoRow = 0x80000000u;
+// Column slices for B much larger than the MALL (launch_vcsr_tile).
+constexpr int32_t kTileSliceCols = 128;
+constexpr uint64_t kTileSliceBytes = 512ull << 20;
 
 template <int R>
 __device__ __forceinline__ void store_vals(float* p, const float (&a)[R]) {
@@ -101,7 +105,7 @@ template <int VEC, int LPE, int R, int MERGE, bool BUF>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu((R <= 3 && MERGE == 1) ? 5 : 1, 8)))
 void vcsr_tile_kernel(
-    int32_t n_chunks, int32_t O, int32_t accumulate, uint32_t b_bytes,
+    int32_t n_chunks, int32_t O, int32_t ld, int32_t accumulate, uint32_t b_bytes,
     const int4* __restrict__ chunks, const int4* __restrict__ pieces,
     const int32_t* __restrict__ ent_brow, const uint16_t* __restrict__ ent_mask,
     const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
@@ -138,7 +142,7 @@ void vcsr_tile_kernel(
 
     // Phase 1: stage the entries (and a one-piece item's padding, buffer
     // path) and the piece table.
-    const uint32_t row_bytes = (uint32_t)O * 4u;
+    const uint32_t row_bytes = (uint32_t)ld * 4u;
     const bool pad = BUF && np == 1;
     const int32_t ne_pad = pad ? (ne + S * U - 1) / (S * U) * (S * U) : ne;  // <= EPAD
     for (int32_t i = lane; i < ne_pad; i += 64) {
@@ -181,7 +185,7 @@ void vcsr_tile_kernel(
             const uint32_t off = (lb[tc] + koff) | (ok ? 0u : kNoRow);
             return load_b_buf<VEC>(rsrc, off);
         } else {
-            const V b = *reinterpret_cast<const V*>(B + (int64_t)lb[tc] * O + koff / 4);
+            const V b = *reinterpret_cast<const V*>(B + (int64_t)lb[tc] * ld + koff / 4);
             return ok ? b : zero_vec(V());
         }
     };
@@ -215,7 +219,7 @@ void vcsr_tile_kernel(
         for (int r = 0; r < R; ++r) {
             if (r >= pc.y) break;
             if (pc.w < 0) {
-                V* dst = reinterpret_cast<V*>(C + (int64_t)(pc.x + r) * O + k);
+                V* dst = reinterpret_cast<V*>(C + (int64_t)(pc.x + r) * ld + k);
                 store_nt(dst, accumulate ? add_vec(*dst, acc[r]) : acc[r]);
             } else {
                 *reinterpret_cast<V*>(partials + (int64_t)(pc.w + r) * O + k) = acc[r];
@@ -379,7 +383,7 @@ void vcsr_tile_kernel(
 // groups are then added in LDS, so a row split into many pieces costs a few
 // load latencies instead of one per piece.
 template <int VEC>
-__global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t O, int32_t accumulate,
+__global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t O, int32_t ld, int32_t accumulate,
                                                         const int4* __restrict__ split,
                                                         const float* __restrict__ partials,
                                                         float* __restrict__ C) {
@@ -415,7 +419,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t O, int32_t accum
             __syncthreads();
         }
         if (g == 0 && cv < nvec) {
-            V* dst = reinterpret_cast<V*>(C + (int64_t)s.x * O + (int64_t)cv * VEC);
+            V* dst = reinterpret_cast<V*>(C + (int64_t)s.x * ld + (int64_t)cv * VEC);
             *dst = accumulate ? add_vec(*dst, red[tid]) : red[tid];
         }
         __syncthreads();
@@ -596,7 +600,7 @@ hipError_t launch_mma(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
 }
 
 template <int VEC, int LPE, int R, bool BUF>
-hipError_t launch_one(const DeviceFmt& d, const float* B, int32_t O, float* C,
+hipError_t launch_one(const DeviceFmt& d, const float* B, int32_t O, int32_t ld, float* C,
                       int32_t accumulate, uint32_t b_bytes, hipStream_t st) {
     // Eight streams per wave (B slices of at most 8 columns) and single-row
     // tiles: four work items per wave, so each stream still gets several
@@ -606,17 +610,17 @@ hipError_t launch_one(const DeviceFmt& d, const float* B, int32_t O, float* C,
     const int64_t waves = ((int64_t)d.tv_n_chunks + MERGE - 1) / MERGE;
     const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves)), block(64 * kWaves);
     hipLaunchKernelGGL((vcsr_tile_kernel<VEC, LPE, R, MERGE, BUF>), grid, block, 0, st, d.tv_n_chunks, O,
-                       accumulate, b_bytes, reinterpret_cast<const int4*>(d.tv_chunks),
+                       ld, accumulate, b_bytes, reinterpret_cast<const int4*>(d.tv_chunks),
                        reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask, d.tv_val, B,
                        C, d.partials);
     return hipGetLastError();
 }
 
 template <int VEC, int R>
-hipError_t launch_r(const DeviceFmt& d, const float* B, int32_t O, float* C, int32_t accumulate,
-                    uint64_t b_bytes, hipStream_t st) {
+hipError_t launch_r(const DeviceFmt& d, const float* B, int32_t O, int32_t ld, float* C,
+                    int32_t accumulate, uint64_t b_bytes, hipStream_t st) {
     if (b_bytes + 64u * 4u * (uint64_t)VEC >= kBufferLimit)
-        return launch_one<VEC, 64, R, false>(d, B, O, C, accumulate, 0u, st);
+        return launch_one<VEC, 64, R, false>(d, B, O, ld, C, accumulate, 0u, st);
     const uint32_t bb = (uint32_t)b_bytes;
     // Lanes per entry: the smallest power of two covering O, at least 8 (at
     // most 8 streams per wave, so every stream gets several tiles).  VEC
@@ -624,33 +628,40 @@ hipError_t launch_r(const DeviceFmt& d, const float* B, int32_t O, float* C, int
     // (or B/C are not 16-byte aligned); then LPE = 8 occurs for VEC = 1 only.
     const int32_t need = (O + VEC - 1) / VEC;
     if constexpr (VEC == 1) {
-        if (need <= 8) return launch_one<VEC, 8, R, true>(d, B, O, C, accumulate, bb, st);
+        if (need <= 8) return launch_one<VEC, 8, R, true>(d, B, O, ld, C, accumulate, bb, st);
     }
-    if (need <= 16) return launch_one<VEC, 16, R, true>(d, B, O, C, accumulate, bb, st);
-    if (need <= 32) return launch_one<VEC, 32, R, true>(d, B, O, C, accumulate, bb, st);
-    return launch_one<VEC, 64, R, true>(d, B, O, C, accumulate, bb, st);
+    if (need <= 16) return launch_one<VEC, 16, R, true>(d, B, O, ld, C, accumulate, bb, st);
+    if (need <= 32) return launch_one<VEC, 32, R, true>(d, B, O, ld, C, accumulate, bb, st);
+    return launch_one<VEC, 64, R, true>(d, B, O, ld, C, accumulate, bb, st);
 }
 
+// Columns [0, O) of B and C, whose rows are ld floats apart (B and C point
+// at the first column; ld > O for one column slice of wider matrices).
 template <int VEC>
-hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, float* C,
-                      int32_t accumulate, hipStream_t st) {
+hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, int32_t ld,
+                      float* C, int32_t accumulate, hipStream_t st) {
     if (d.tv_n_chunks > 0) {
-        const uint64_t b_bytes = (uint64_t)v.N * (uint64_t)O * 4u;
+        // Bytes from B to the end of its last row.
+        const uint64_t b_bytes = v.N > 0 ? ((uint64_t)(v.N - 1) * (uint64_t)ld + (uint64_t)O) * 4u : 0u;
         hipError_t e;
         switch (d.tv_R) {
-            case 1: e = launch_r<VEC, 1>(d, B, O, C, accumulate, b_bytes, st); break;
-            case 2: e = launch_r<VEC, 2>(d, B, O, C, accumulate, b_bytes, st); break;
-            case 3: e = launch_r<VEC, 3>(d, B, O, C, accumulate, b_bytes, st); break;
-            case 4: e = launch_r<VEC, 4>(d, B, O, C, accumulate, b_bytes, st); break;
-            case 8: e = launch_r<VEC, 8>(d, B, O, C, accumulate, b_bytes, st); break;
-            case kTileMmaRows: e = launch_mma<VEC>(v, d, B, O, C, accumulate, st); break;
+            case 1: e = launch_r<VEC, 1>(d, B, O, ld, C, accumulate, b_bytes, st); break;
+            case 2: e = launch_r<VEC, 2>(d, B, O, ld, C, accumulate, b_bytes, st); break;
+            case 3: e = launch_r<VEC, 3>(d, B, O, ld, C, accumulate, b_bytes, st); break;
+            case 4: e = launch_r<VEC, 4>(d, B, O, ld, C, accumulate, b_bytes, st); break;
+            case 8: e = launch_r<VEC, 8>(d, B, O, ld, C, accumulate, b_bytes, st); break;
+            case kTileMmaRows:
+                // 16-row tiles are never column-sliced: their rows are O apart.
+                if (ld != O) return hipErrorInvalidValue;
+                e = launch_mma<VEC>(v, d, B, O, C, accumulate, st);
+                break;
             default: return hipErrorInvalidValue;
         }
         if (e != hipSuccess) return e;
     }
     if (d.tv_n_split > 0) {
         hipLaunchKernelGGL(vcsr_tile_reduce<VEC>, dim3((unsigned)d.tv_n_split), dim3(256), 0, st,
-                           O, accumulate, reinterpret_cast<const int4*>(d.tv_split), d.partials,
+                           O, ld, accumulate, reinterpret_cast<const int4*>(d.tv_split), d.partials,
                            C);
         return hipGetLastError();
     }
@@ -675,11 +686,26 @@ hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, i
     // Narrow B: narrower per-lane vectors give streams of at least 8-16
     // lanes, so fewer streams share a tile's entries (measured at O = 8:
     // 4-byte loads with 8 streams 1.3x faster than 16-byte loads with 32).
-    switch (tile_vec(O, a16, a8)) {
-        case 4: return launch_vec<4>(v, d, B, O, C, accumulate, st);
-        case 2: return launch_vec<2>(v, d, B, O, C, accumulate, st);
-        default: return launch_vec<1>(v, d, B, O, C, accumulate, st);
+    const int vec = tile_vec(O, a16, a8);
+    // B much larger than the MALL (256 MB) on single-row to 8-row tiles:
+    // column slices of kTileSliceCols, one launch each, so the B rows that
+    // are live at a time take half the bytes (measured on the uniform-random
+    // 1M x 1M matrix at O = 256: 2 slices 13% faster than one pass).
+    const int32_t W = (vec == 4 && d.tv_R != kTileMmaRows && O > kTileSliceCols &&
+                       (uint64_t)v.N * (uint64_t)O * 4u > kTileSliceBytes)
+                          ? kTileSliceCols
+                          : O;
+    for (int32_t c0 = 0; c0 < O; c0 += W) {
+        const int32_t w = std::min(W, O - c0);
+        hipError_t e;
+        switch (vec) {
+            case 4: e = launch_vec<4>(v, d, B + c0, w, O, C + c0, accumulate, st); break;
+            case 2: e = launch_vec<2>(v, d, B + c0, w, O, C + c0, accumulate, st); break;
+            default: e = launch_vec<1>(v, d, B + c0, w, O, C + c0, accumulate, st); break;
+        }
+        if (e != hipSuccess) return e;
     }
+    return hipSuccess;
 }
 
 MfmaWork tile_mfma_work(const DeviceFmt& d, int32_t O) {
