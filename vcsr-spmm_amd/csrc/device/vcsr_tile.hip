@@ -48,7 +48,9 @@ constexpr int kWaves = 4;
 // Buffer offset of "no B row": at least 2^31, above any buffer-path B size,
 // and still below 2^32 after adding a column offset (< 2^31).
 constexpr uint32_t kNoRow = 0x80000000u;
-// Column slices for B much larger than the MALL (launch_vcsr_tile).
+// Column slices (launch_vcsr_tile): at most kTileWideCols columns per
+// launch, and kTileSliceCols when B is over twice the MALL's 256 MB.
+constexpr int32_t kTileWideCols = 256;
 constexpr int32_t kTileSliceCols = 128;
 constexpr uint64_t kTileSliceBytes = 512ull << 20;
 
@@ -687,14 +689,18 @@ hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, i
     // lanes, so fewer streams share a tile's entries (measured at O = 8:
     // 4-byte loads with 8 streams 1.3x faster than 16-byte loads with 32).
     const int vec = tile_vec(O, a16, a8);
-    // B much larger than the MALL (256 MB) on single-row to 8-row tiles:
-    // column slices of kTileSliceCols, one launch each, so the B rows that
-    // are live at a time take half the bytes (measured on the uniform-random
-    // 1M x 1M matrix at O = 256: 2 slices 13% faster than one pass).
-    const int32_t W = (vec == 4 && d.tv_R != kTileMmaRows && O > kTileSliceCols &&
-                       (uint64_t)v.N * (uint64_t)O * 4u > kTileSliceBytes)
-                          ? kTileSliceCols
-                          : O;
+    // Tiles of 1 to 8 rows with 16-byte vectors: one launch per column slice
+    // of at most 256 columns (one column tile of a wave), or 128 when B is
+    // over 512 MB, so that the B bytes live at a time stay small.  Measured
+    // against one launch over all columns: banded 62K matrix, slices of 256,
+    // O = 512 / 1024 / 2048: same / 16% / 30% faster; slices of 128,
+    // uniform-random 1M matrix O = 256 (1 GB): 11% faster, power-law 322K
+    // matrix O = 512 (659 MB): 3% faster, O = 256 (330 MB): 3% slower.
+    int32_t W = O;
+    if (vec == 4 && d.tv_R != kTileMmaRows) {
+        if ((uint64_t)v.N * (uint64_t)O * 4u > kTileSliceBytes) W = std::min(O, kTileSliceCols);
+        else W = std::min(O, kTileWideCols);
+    }
     for (int32_t c0 = 0; c0 < O; c0 += W) {
         const int32_t w = std::min(W, O - c0);
         hipError_t e;
