@@ -117,7 +117,10 @@ void vcsr_tile_kernel(
     constexpr int RS = tile_slot_stride(R);                  // slots stored per entry
     constexpr int EMAX = tile_piece_entries(R) * MERGE;      // entries per wave
     constexpr int PMAX = kTileChunkPieces * MERGE;           // pieces per wave
-    constexpr int U = 8;                                     // loads per block
+    // Loads per block: 8, or 4 when 8+ streams split a tall tile's entries
+    // (fewer padded entries per block: banded 62K matrix, O = 8 / 32, 3%
+    // faster; single-row tiles, which merge four items, measured slower).
+    constexpr int U = (S >= 8 && R > 1) ? 4 : 8;
     // A one-piece item's list is padded with "no row" entries of value 0 up
     // to a multiple of S*U, so that all its blocks are full blocks.
     constexpr int EPAD = (EMAX + S * U - 1) / (S * U) * (S * U);
@@ -625,11 +628,10 @@ hipError_t launch_r(const DeviceFmt& d, const float* B, int32_t O, int32_t ld, f
         return launch_one<VEC, 64, R, false>(d, B, O, ld, C, accumulate, 0u, st);
     const uint32_t bb = (uint32_t)b_bytes;
     // Lanes per entry: the smallest power of two covering O, at least 8 (at
-    // most 8 streams per wave, so every stream gets several tiles).  VEC
-    // below 4 is chosen only when O is too narrow for 16 lanes of 4 floats
-    // (or B/C are not 16-byte aligned); then LPE = 8 occurs for VEC = 1 only.
+    // most 8 streams per wave, so every stream gets several tiles); 8 lanes
+    // occur for VEC = 4 (O = 32) and VEC = 1 (O <= 8).
     const int32_t need = (O + VEC - 1) / VEC;
-    if constexpr (VEC == 1) {
+    if constexpr (VEC == 1 || VEC == 4) {
         if (need <= 8) return launch_one<VEC, 8, R, true>(d, B, O, ld, C, accumulate, bb, st);
     }
     if (need <= 16) return launch_one<VEC, 16, R, true>(d, B, O, ld, C, accumulate, bb, st);
@@ -672,10 +674,12 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
 
 }  // namespace
 
-// Floats per lane and B slice: 4 when O allows 16 lanes of 16-byte vectors
-// and B and C are 16-byte aligned, else 2 or 1.
-static int tile_vec(int32_t O, bool a16, bool a8) {
-    if (O % 4 == 0 && a16 && O >= 64) return 4;
+// Floats per lane and B slice: 4 when O allows 8 lanes (16 for 16-row MFMA
+// tiles, whose column tiles are 16 lanes wide) of 16-byte vectors and B and
+// C are 16-byte aligned, else 2 or 1.  At O = 32, 4 floats per lane measured
+// 3% / 8% faster than 2 on the banded / power-law matrices.
+static int tile_vec(int32_t O, bool a16, bool a8, bool mma) {
+    if (O % 4 == 0 && a16 && O >= (mma ? 64 : 32)) return 4;
     if (O % 2 == 0 && a8 && O >= 32) return 2;
     return 1;
 }
@@ -688,7 +692,7 @@ hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, i
     // Narrow B: narrower per-lane vectors give streams of at least 8-16
     // lanes, so fewer streams share a tile's entries (measured at O = 8:
     // 4-byte loads with 8 streams 1.3x faster than 16-byte loads with 32).
-    const int vec = tile_vec(O, a16, a8);
+    const int vec = tile_vec(O, a16, a8, d.tv_R == kTileMmaRows);
     // Tiles of 1 to 8 rows with 16-byte vectors: one launch per column slice
     // of at most 256 columns (one column tile of a wave), or 128 when B is
     // over 512 MB, so that the B bytes live at a time stay small.  Measured
@@ -718,7 +722,7 @@ MfmaWork tile_mfma_work(const DeviceFmt& d, int32_t O) {
     MfmaWork w;
     w.flops_per_op = 2 * 16 * 16 * 4;
     if (d.tv_R != kTileMmaRows || O <= 0) return w;
-    const int vec = tile_vec(O, true, true);
+    const int vec = tile_vec(O, true, true, true);
     const int64_t n_ct = (O + 16 * vec - 1) / (16 * vec);
     w.ops = d.tv_n_entries / 4 * n_ct * vec;
     return w;
