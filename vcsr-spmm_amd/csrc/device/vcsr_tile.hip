@@ -34,6 +34,7 @@
 // non-finite is recomputed with the presence bits before it is stored, so
 // inf / NaN in B reach exactly the rows the reference's loop reaches.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "../host/tile_view.hpp"
@@ -48,6 +49,20 @@ constexpr int kWaves = 4;
 // Buffer offset of "no B row": at least 2^31, above any buffer-path B size,
 // and still below 2^32 after adding a column offset (< 2^31).
 constexpr uint32_t kNoRow = 0x80000000u;
+// Compute units of a device (256 on MI355X), read once per device.
+int device_cus(int device) {
+    static std::atomic<int> cus[64];
+    if (device < 0 || device >= 64) return 256;
+    int n = cus[device].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[device].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 // Column slices (launch_vcsr_tile): at most kTileWideCols columns per
 // launch, and kTileSliceCols when B is over twice the MALL's 256 MB.
 constexpr int32_t kTileWideCols = 256;
@@ -458,7 +473,11 @@ __device__ __forceinline__ float vec_part(const typename VecT<VEC>::T& b, int c)
     return reinterpret_cast<const float*>(&b)[c];
 }
 
-template <int VEC, bool BUF>
+// GU entry groups (of 16) per block of loads.  SB: a scheduling barrier
+// keeps the block's loads ahead of its MFMAs (more loads in flight per wave,
+// more registers); without it the compiler interleaves them and the kernel
+// fits 8 waves per SIMD.
+template <int VEC, bool BUF, int GU, bool SB>
 __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
     int32_t n_items, int32_t n_ctiles, int32_t O, int32_t accumulate, uint32_t b_bytes,
     const int4* __restrict__ chunks, const int4* __restrict__ pieces,
@@ -466,7 +485,6 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
     const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
     float* __restrict__ partials) {
     using V = typename VecT<VEC>::T;
-    constexpr int GU = 4;  // entry groups (of 16) per block of loads
     __shared__ uint32_t s_brow[kMmaWaves][kMmaPiece];
 
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -522,6 +540,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
 #pragma unroll
             for (int s = 0; s < 4; ++s) b[gu][s] = load_b(16 * (g0 + gu) + 4 * s + kq);
         }
+        if constexpr (SB) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int gu = 0; gu < NG; ++gu)
 #pragma unroll
@@ -583,24 +602,48 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
     }
 }
 
+template <int VEC, bool BUF, int GU, bool SB>
+void launch_mma_as(const DeviceFmt& d, dim3 grid, int32_t n_ct, int32_t O, int32_t accumulate,
+                   uint32_t b_bytes, const float* B, float* C, hipStream_t st) {
+    hipLaunchKernelGGL((vcsr_tile_mma_kernel<VEC, BUF, GU, SB>), grid, dim3(64 * kMmaWaves), 0, st,
+                       d.tv_n_chunks, n_ct, O, accumulate, b_bytes,
+                       reinterpret_cast<const int4*>(d.tv_chunks),
+                       reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask, d.tv_val,
+                       B, C, d.partials);
+}
+
+template <int VEC, bool BUF>
+void launch_mma_buf(const DeviceFmt& d, dim3 grid, int64_t waves, int32_t n_ct, int32_t O,
+                    int32_t accumulate, uint32_t b_bytes, const float* B, float* C,
+                    hipStream_t st) {
+    // Few waves per SIMD (cfg5-like matrices at O <= 192): each wave's loads
+    // in flight bound the time, so its loads go ahead of its MFMAs; with
+    // many, 8 waves per SIMD with interleaved loads hide the latency better.
+    // Measured on the 16K block-sparse matrix (1,024 tiles): O = 32 / 64,
+    // one wave per SIMD, 4 groups with the barrier 27% / 36% faster; O = 128
+    // / 192, two or three, 2 groups with the barrier 20% / 4% faster; O >= 256
+    // slower with the barrier (O = 512: 236 / 186 against 152 us).
+    const int64_t simds = 4 * (int64_t)device_cus(d.device);
+    if (waves <= simds)
+        launch_mma_as<VEC, BUF, 4, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
+    else if (waves <= 3 * simds)
+        launch_mma_as<VEC, BUF, 2, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
+    else
+        launch_mma_as<VEC, BUF, 4, false>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
+}
+
 template <int VEC>
 hipError_t launch_mma(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, float* C,
                       int32_t accumulate, hipStream_t st) {
     const int32_t n_ct = (O + 16 * VEC - 1) / (16 * VEC);
     const int64_t waves = (int64_t)d.tv_n_chunks * n_ct;
-    const dim3 grid((unsigned)((waves + kMmaWaves - 1) / kMmaWaves)), block(64 * kMmaWaves);
+    const dim3 grid((unsigned)((waves + kMmaWaves - 1) / kMmaWaves));
     const uint64_t b_bytes = (uint64_t)v.N * (uint64_t)O * 4u;
     if (b_bytes + 64u * 4u * (uint64_t)VEC >= kBufferLimit)
-        hipLaunchKernelGGL((vcsr_tile_mma_kernel<VEC, false>), grid, block, 0, st, d.tv_n_chunks,
-                           n_ct, O, accumulate, 0u, reinterpret_cast<const int4*>(d.tv_chunks),
-                           reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask,
-                           d.tv_val, B, C, d.partials);
+        launch_mma_buf<VEC, false>(d, grid, waves, n_ct, O, accumulate, 0u, B, C, st);
     else
-        hipLaunchKernelGGL((vcsr_tile_mma_kernel<VEC, true>), grid, block, 0, st, d.tv_n_chunks,
-                           n_ct, O, accumulate, (uint32_t)b_bytes,
-                           reinterpret_cast<const int4*>(d.tv_chunks),
-                           reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask,
-                           d.tv_val, B, C, d.partials);
+        launch_mma_buf<VEC, true>(d, grid, waves, n_ct, O, accumulate, (uint32_t)b_bytes, B, C,
+                                  st);
     return hipGetLastError();
 }
 
