@@ -5,10 +5,12 @@ Workload (the headline): banded FEM-like A, 62,451^2,
 layout S with segw=4, bundle=64, tileK=64, built and uploaded before timing.
 
 A step is one complete SpMM C = A*B on device-resident inputs.  The default
-kernel (spmm_vcsr_ex, VCSR_KERNEL_AUTO = the row-stationary VCSR kernel with
-accumulate = 0) writes every element of C, so a step is one launch; the
-kernels that accumulate into C as the reference's do (--algo segment / mfma)
-get a C reset inside the step.  K steps are timed between HIP events after W
+kernel (spmm_vcsr_ex, VCSR_KERNEL_AUTO = the tile-stationary VCSR kernel,
+16-row tiles on FP32 MFMA where the row-tile view has them, accumulate = 0)
+writes every element of C, so a step is its launches alone (one per column
+slice, plus the reduce kernel where tiles are split); the kernels that
+accumulate into C as the reference's do (--algo segment / mfma) get a C
+reset inside the step.  --cols replaces a config's O (column sweeps).  K steps are timed between HIP events after W
 warm-up steps; `value` is 2*nnz*O*K / that time.  `kernel_ms` is the kernel
 alone, K back-to-back launches between events on its stream (the reference
 times kernels only, src/kernels.cu:153-162); the roofline uses it.
@@ -63,17 +65,18 @@ def log(msg):
 
 
 def measured_traffic(config, algo):
-    """HBM-side bytes per launch of the dominant kernel, from the committed
+    """HBM-side bytes per SpMM of the dominant kernel, from the committed
     rocprofv3 counter summary (profiles/traffic.json): FETCH_SIZE and
-    WRITE_SIZE of the kernel, each divided by what the same counter reads
-    per byte for a device-to-device copy of known size.  None if absent."""
+    WRITE_SIZE per dispatch, each divided by what the same counter reads per
+    byte for a device-to-device copy of known size, times the kernel's
+    dispatches per SpMM (column slices).  None if absent."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
         e = t["kernels"][f"{config}/{algo}"]
-        return (e["fetch_kib"] * 1024.0 / t["copy_fetch_factor"] +
-                e["write_kib"] * 1024.0 / t["copy_write_factor"])
+        return e.get("launches", 1) * (e["fetch_kib"] * 1024.0 / t["copy_fetch_factor"] +
+                                       e["write_kib"] * 1024.0 / t["copy_write_factor"])
     except (OSError, KeyError, ValueError, ZeroDivisionError):
         return None
 
@@ -101,6 +104,8 @@ def main():
                     choices=["vcsr", "tile", "row", "segment", "mfma", "fast", "csr", "aspt",
                              "rocsparse"])
     ap.add_argument("--tileK", type=int, default=None)
+    ap.add_argument("--cols", type=int, default=None, metavar="O",
+                    help="columns of B and C instead of the config's O")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -137,6 +142,8 @@ def main():
     cfg, O, segw, bundle, tileK, layout, dist = CONFIGS[args.config]
     if args.tileK:
         tileK = args.tileK
+    if args.cols:
+        O = args.cols
     log(f"bench: {args.config} algo={args.algo} O={O} segw={segw} bundle={bundle} "
         f"tileK={tileK} device={vs.device_name()}")
     t0 = time.perf_counter()
@@ -278,7 +285,8 @@ def main():
         "check": {"rel_l2_sampled_rows": rel, "result": check},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(args.config, args.algo),
+                     "traffic": (measured_traffic(args.config, args.algo)
+                                 if O == CONFIGS[args.config][1] else None),
                      "bytes_alg": bytes_alg},
     }
     # The tile-stationary kernel runs 16-row tiles on the matrix cores.
