@@ -166,6 +166,19 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
         std::vector<int32_t> tv_brow(tv.brow);
         for (size_t q = 0; q < tv_brow.size(); ++q)
             if (tv.mask[q] == 0) tv_brow[q] = vcsr::kTileNoEntry;
+        // Device values: for 1- and 3-row tiles each entry's B row follows
+        // its values (vcsr::tile_dev_stride).
+        std::vector<float> tv_val;
+        if (vcsr::tile_dev_folds_brow(tv.R)) {
+            const int32_t rs = vcsr::tile_slot_stride(tv.R), ds = vcsr::tile_dev_stride(tv.R);
+            const size_t E = tv_brow.size();
+            tv_val.assign(E * (size_t)ds, 0.f);
+            for (size_t q = 0; q < E; ++q) {
+                for (int32_t r = 0; r < tv.R; ++r)
+                    tv_val[q * ds + r] = tv.val[q * rs + r];
+                std::memcpy(&tv_val[q * ds + ds - 1], &tv_brow[q], sizeof(float));
+            }
+        }
         DeviceFmt d;
         hip_check(hipGetDevice(&d.device), "hipGetDevice");
         try {
@@ -192,7 +205,8 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.tv_n_chunks = (int32_t)(tv.chunks.size() / 4);
             d.tv_pieces = upload_array(tv.pieces, st, "upload tile pieces");
             d.tv_brow = upload_array(tv_brow, st, "upload tile entries");
-            d.tv_val = upload_array(tv.val, st, "upload tile values");
+            d.tv_val = upload_array(vcsr::tile_dev_folds_brow(tv.R) ? tv_val : tv.val, st,
+                                    "upload tile values");
             d.tv_mask = upload_array(tv.mask, st, "upload tile masks");
             d.tv_n_entries = tv.n_entries();
             d.tv_split = upload_array(tv.split, st, "upload split tiles");

@@ -130,6 +130,8 @@ void vcsr_tile_kernel(
     using V = typename VecT<VEC>::T;
     constexpr int S = 64 / LPE;                              // streams per wave
     constexpr int RS = tile_slot_stride(R);                  // slots stored per entry
+    constexpr bool FOLD = tile_dev_folds_brow(R);            // B row inside the values
+    constexpr int DS = tile_dev_stride(R);                   // floats per entry in ent_val
     constexpr int EMAX = tile_piece_entries(R) * MERGE;      // entries per wave
     constexpr int PMAX = kTileChunkPieces * MERGE;           // pieces per wave
     // Loads per block: 8, or 4 when 8+ streams split a tall tile's entries
@@ -170,8 +172,18 @@ void vcsr_tile_kernel(
         float a[RS];
         if (i < ne) {
             const int64_t e = (int64_t)e0 + i;
-            br = (uint32_t)ent_brow[e];
-            load_vals<RS>(ent_val + e * RS, a);
+            if constexpr (FOLD) {
+                // One load: the values, then the B row's bits (for 3 rows in
+                // the padding slot, which the FMAs never read).
+                float rec[DS];
+                load_vals<DS>(ent_val + e * DS, rec);
+                br = __builtin_bit_cast(uint32_t, rec[DS - 1]);
+#pragma unroll
+                for (int q = 0; q < RS; ++q) a[q] = rec[q];
+            } else {
+                br = (uint32_t)ent_brow[e];
+                load_vals<RS>(ent_val + e * RS, a);
+            }
         } else {
 #pragma unroll
             for (int q = 0; q < RS; ++q) a[q] = 0.f;
@@ -181,13 +193,15 @@ void vcsr_tile_kernel(
         lb[i] = BUF ? (real ? br * row_bytes : kNoRow) : (real ? br : 0u);
         store_vals<RS>(lv + i * RS, a);
     }
-    for (int32_t j = lane; j < np; j += 64) {
-        int4 pc = pieces[p0 + j];
-        pc.z -= e0;
-        lp[j] = pc;
-        lbad[j] = 0;
+    if (np > 1) {
+        for (int32_t j = lane; j < np; j += 64) {
+            int4 pc = pieces[p0 + j];
+            pc.z -= e0;
+            lp[j] = pc;
+            lbad[j] = 0;
+        }
+        if (lane < 2) lp[np + lane] = make_int4(0, 0, ne, -1);  // end sentinels
     }
-    if (lane < 2) lp[np + lane] = make_int4(0, 0, ne, -1);  // end sentinels
     wave_sync();
 
     const __amdgpu_buffer_rsrc_t rsrc =
@@ -230,10 +244,9 @@ void vcsr_tile_kernel(
         for (int r = 0; r < R; ++r) z = fma_zero_acc(acc[r], z);
         return __builtin_isfinite(z) || !kok;
     };
-    // Writes the accumulated rows of piece pidx (its first pc.y rows exist)
-    // to C or to its partial rows.
-    auto store_piece = [&](int32_t pidx, const V (&acc)[R], int32_t k, bool kok) {
-        const int4 pc = lp[pidx];
+    // Writes the accumulated rows of piece pc (its first pc.y rows exist) to
+    // C or to its partial rows.
+    auto store_piece = [&](const int4 pc, const V (&acc)[R], int32_t k, bool kok) {
         if (!kok) return;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -246,13 +259,15 @@ void vcsr_tile_kernel(
             }
         }
     };
-    // Exact recomputation of piece q in entry order, skipping absent rows
-    // (taken only for pieces whose sum is not finite, which were not stored).
-    auto redo_piece = [&](int32_t q, int32_t k, uint32_t koff, bool kok) {
+    // Exact recomputation of piece pc (entries tb .. te-1) in entry order,
+    // skipping absent rows (taken only for pieces whose sum is not finite,
+    // which were not stored).
+    auto redo_piece = [&](const int4 pc, int32_t tb, int32_t te, int32_t k, uint32_t koff,
+                          bool kok) {
         V acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
-        for (int32_t t = lp[q].z; t < lp[q + 1].z; ++t) {
+        for (int32_t t = tb; t < te; ++t) {
             const V b = load_b(t, true, koff);
             float a[RS];
             load_vals<RS>(lv + t * RS, a);
@@ -261,7 +276,7 @@ void vcsr_tile_kernel(
             for (int r = 0; r < R; ++r)
                 if ((m >> r) & 1u) fma_vec(acc[r], a[r], b);
         }
-        store_piece(q, acc, k, kok);
+        store_piece(pc, acc, k, kok);
     };
 
     if (np > 1) {
@@ -323,7 +338,7 @@ void vcsr_tile_kernel(
                             bad = true;
                             lbad[p] = 1;
                         } else {
-                            store_piece(p, acc, k, kok);
+                            store_piece(lp[p], acc, k, kok);
                         }
 #pragma unroll
                         for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
@@ -339,7 +354,7 @@ void vcsr_tile_kernel(
             if (__any(bad)) {
                 wave_sync();
                 for (int32_t q = pa; q < pb; ++q)
-                    if (lbad[q]) redo_piece(q, k, koff, kok);
+                    if (lbad[q]) redo_piece(lp[q], lp[q].z, lp[q + 1].z, k, koff, kok);
                 wave_sync();
                 for (int32_t q = pa; q < pb; ++q) lbad[q] = 0;
                 wave_sync();
@@ -347,6 +362,9 @@ void vcsr_tile_kernel(
         }
     } else {
         // One piece: entries t = sub + S*i, summed across streams at the end.
+        // Its record is wave-uniform (scalar loads; no LDS table).
+        const int4 pc1 = make_int4(uniform(pieces[p0].x), uniform(pieces[p0].y),
+                                   uniform(pieces[p0].z) - e0, uniform(pieces[p0].w));
         const int32_t nper = (ne + S - 1) / S, nfull = ne / S;
         for (int32_t k0 = 0; k0 < O; k0 += LPE * VEC) {
             const int32_t k = k0 + kl * VEC;
@@ -388,9 +406,9 @@ void vcsr_tile_kernel(
             // its lanes' values is not finite.
             const bool bad = sub == 0 && !piece_finite(acc, kok);
             if (__any(bad)) {
-                if (sub == 0) redo_piece(0, k, koff, kok);
+                if (sub == 0) redo_piece(pc1, pc1.z, ne, k, koff, kok);
             } else if (sub == 0) {
-                store_piece(0, acc, k, kok);
+                store_piece(pc1, acc, k, kok);
             }
         }
     }

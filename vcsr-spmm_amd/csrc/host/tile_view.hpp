@@ -64,6 +64,13 @@ constexpr int32_t kTileChunkPieces = 32;
 // B row of a placeholder entry (no tile row present) in the device copy of
 // the view's B-row array; the host view keeps 0 there.
 constexpr int32_t kTileNoEntry = -1;
+// The device copy of the values of 1- and 3-row tiles also holds each
+// entry's B row (kTileNoEntry for placeholders), as the bits of one more
+// float after its values — for 3 rows in the padding slot of the stride —
+// so that one load gives an entry's B row and values.  Floats per entry
+// there:
+constexpr bool tile_dev_folds_brow(int32_t R) { return R == 1 || R == 3; }
+constexpr int32_t tile_dev_stride(int32_t R) { return R == 1 ? 2 : tile_slot_stride(R); }
 // Rows are cut into tiles inside fixed blocks of this many rows (so that
 // blocks can be tiled in parallel and the view never depends on the thread
 // count).
