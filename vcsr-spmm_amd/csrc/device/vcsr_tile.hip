@@ -139,7 +139,9 @@ void vcsr_tile_kernel(
     // faster; single-row tiles, which merge four items, measured slower).
     constexpr int U = (S >= 8 && R > 1) ? 4 : 8;
     // A one-piece item's list is padded with "no row" entries of value 0 up
-    // to a multiple of S*U, so that all its blocks are full blocks.
+    // to a multiple of S*UT, so that its blocks are full blocks of U loads
+    // per stream and at most one of UT (UT = U/2 for U = 8).
+    constexpr int UT = U >= 8 ? U / 2 : U;
     constexpr int EPAD = (EMAX + S * U - 1) / (S * U) * (S * U);
     __shared__ uint32_t s_brow[kWaves][EPAD];
     __shared__ uint8_t s_bad[kWaves][PMAX];
@@ -166,7 +168,7 @@ void vcsr_tile_kernel(
     // path) and the piece table.
     const uint32_t row_bytes = (uint32_t)ld * 4u;
     const bool pad = BUF && np == 1;
-    const int32_t ne_pad = pad ? (ne + S * U - 1) / (S * U) * (S * U) : ne;  // <= EPAD
+    const int32_t ne_pad = pad ? (ne + S * UT - 1) / (S * UT) * (S * UT) : ne;  // <= EPAD
     for (int32_t i = lane; i < ne_pad; i += 64) {
         uint32_t br = (uint32_t)kTileNoEntry;
         float a[RS];
@@ -390,7 +392,22 @@ void vcsr_tile_kernel(
                 }
             };
             if constexpr (BUF) {
-                for (int32_t i0 = 0; i0 < ne_pad / S; i0 += U) block(std::true_type(), i0);
+                // Full blocks of U loads per stream, then one of UT if the
+                // padded list has that many left.
+                auto block_n = [&](auto nu_c, int32_t i0) {
+                    constexpr int NU = decltype(nu_c)::value;
+                    V b[NU];
+#pragma unroll
+                    for (int u = 0; u < NU; ++u) b[u] = load_b(sub + S * (i0 + u), true, koff);
+#pragma unroll
+                    for (int u = 0; u < NU; ++u) apply(acc, sub + S * (i0 + u), true, b[u]);
+                };
+                const int32_t nper_pad = ne_pad / S;
+                int32_t i0 = 0;
+                for (; i0 + U <= nper_pad; i0 += U) block_n(std::integral_constant<int, U>(), i0);
+                if constexpr (UT < U) {
+                    if (i0 < nper_pad) block_n(std::integral_constant<int, UT>(), i0);
+                }
             } else {
                 for (int32_t i0 = 0; i0 < nper; i0 += U) {
                     if (i0 + U <= nfull) block(std::true_type(), i0);
