@@ -140,8 +140,8 @@ void vcsr_tile_kernel(
     constexpr int U = (S >= 8 && R > 1) ? 4 : 8;
     // A one-piece item's list is padded with "no row" entries of value 0 up
     // to a multiple of S*UT, so that its blocks are full blocks of U loads
-    // per stream and at most one of UT (UT = U/2 for U = 8).
-    constexpr int UT = U >= 8 ? U / 2 : U;
+    // per stream and at most one each of U/2, U/4, ... UT (UT = 2).
+    constexpr int UT = U >= 2 ? 2 : U;
     constexpr int EPAD = (EMAX + S * U - 1) / (S * U) * (S * U);
     __shared__ uint32_t s_brow[kWaves][EPAD];
     __shared__ uint8_t s_bad[kWaves][PMAX];
@@ -405,8 +405,14 @@ void vcsr_tile_kernel(
                 const int32_t nper_pad = ne_pad / S;
                 int32_t i0 = 0;
                 for (; i0 + U <= nper_pad; i0 += U) block_n(std::integral_constant<int, U>(), i0);
-                if constexpr (UT < U) {
-                    if (i0 < nper_pad) block_n(std::integral_constant<int, UT>(), i0);
+                if constexpr (U / 2 >= UT) {
+                    if (i0 + U / 2 <= nper_pad) {
+                        block_n(std::integral_constant<int, U / 2>(), i0);
+                        i0 += U / 2;
+                    }
+                }
+                if constexpr (U / 4 >= UT) {
+                    if (i0 + U / 4 <= nper_pad) block_n(std::integral_constant<int, U / 4>(), i0);
                 }
             } else {
                 for (int32_t i0 = 0; i0 < nper; i0 += U) {
