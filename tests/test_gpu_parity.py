@@ -656,6 +656,32 @@ def test_mfma_tiles_are_bit_exact(gpu, orc, st, fixed, O):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("O", [64, 128, 512])
+def test_mfma_schedules_by_waves_per_simd_are_bit_exact(gpu, orc, st, O):
+    """The 16-row MFMA tiles run with one of three load schedules, chosen by
+    waves per SIMD (1,024 SIMDs on MI355X): the full cfg5 matrix (1,024 tiles
+    of 816 entries) has 1,024 waves at O = 64 (4 groups per block, loads kept
+    ahead of the MFMAs), 2,048 at O = 128 (2 groups, kept ahead) and 8,192 at
+    O = 512 (4 groups, interleaved by the compiler).  Each gives the oracle's
+    FP32 loop bit for bit on 400 sampled rows and the first and last row."""
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(5, 0))
+    B = vs.gen_dense(5, 1, csr.N, O)
+    fmt = vs.build_vcsr(csr, 16, 16, vs.LAYOUT_TC)
+    fmt.upload(st)
+    R, tiles, entries = fmt.tile_info()
+    assert (R, tiles) == (16, 1024) and entries <= tiles * 1024
+    got = _ex(vs, fmt, B, np.zeros((csr.M, O), np.float32), st, vs.KERNEL_TILE, False)
+    rng = np.random.default_rng(O)
+    rows = np.unique(np.concatenate([rng.choice(csr.M, 400, replace=False), [0, csr.M - 1]]))
+    n = np.diff(csr.row_ptr)[rows]
+    rp = np.concatenate([[0], np.cumsum(n)]).astype(np.int32)
+    sc = np.concatenate([csr.col[csr.row_ptr[r]:csr.row_ptr[r + 1]] for r in rows])
+    sv = np.concatenate([csr.val[csr.row_ptr[r]:csr.row_ptr[r + 1]] for r in rows])
+    ref = orc.spmm_f32(len(rows), rp, sc, sv, B)
+    assert np.array_equal(got[rows].view(np.uint32), ref.view(np.uint32))
+
+
 from hypothesis import HealthCheck, given, settings
 from hypothesis import strategies as hst
 
