@@ -14,25 +14,32 @@
 // Work item (one wave): MERGE consecutive work items of the view, each a run
 // of tile pieces with at most tile_piece_entries(R) entries
 // (host/tile_view.hpp).
-// Phase 1 (lane per entry): read the entry's B row, presence bits and R
-// values (the view stores the values of its slots next to each other, so
-// these are coalesced loads, not gathers from the VCSR value array) and stage
-// (B-row byte offset, presence bits, values) in the wave's LDS list.
+// Phase 1 (lane per entry): read the entry's B row and R values (the view
+// stores the values of its slots next to each other, for 1- and 3-row tiles
+// in one record with the B row, so these are coalesced loads, not gathers
+// from the VCSR value array) and stage (B-row byte offset, values) in the
+// wave's LDS list.
 // Phase 2, per column tile of LPE*VEC columns: the wave is S = 64/LPE
 // streams of LPE lanes; one load instruction serves one entry of every
 // stream.
 //  - Several pieces: each stream takes a contiguous run of whole pieces
 //    (balanced by entry count), accumulates the piece's R rows and stores
 //    them when its last entry has been applied.  No cross-lane reduction.
-//  - One piece (a long tile): the streams interleave over its entries and
-//    their sums are added with cross-lane shuffles before the store.
+//  - One piece (a long tile): the streams interleave over its entries, whose
+//    list is padded to whole blocks, and their sums are added with
+//    cross-lane shuffles before the store.
 // Loads are issued in blocks of U back to back before the block's FMAs; B is
 // read with raw buffer loads whose range check turns out-of-range offsets
 // into zeros, so inactive lanes and placeholder entries need no branch.
 // Rows absent from an entry are updated with a zero value (no per-row
 // select); this is exact for finite B.  A piece whose sum comes out
-// non-finite is recomputed with the presence bits before it is stored, so
-// inf / NaN in B reach exactly the rows the reference's loop reaches.
+// non-finite is recomputed with the presence bits (read from global memory
+// on that rare path) before it is stored, so inf / NaN in B reach exactly
+// the rows the reference's loop reaches.
+//
+// The host launcher runs one launch per column slice of at most 256
+// columns (128 when B is over 512 MB); tiles of 16 rows go to the MFMA
+// kernel further down.
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
