@@ -204,7 +204,9 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.tv_chunks = upload_array(tv.chunks, st, "upload tile chunks");
             d.tv_n_chunks = (int32_t)(tv.chunks.size() / 4);
             d.tv_pieces = upload_array(tv.pieces, st, "upload tile pieces");
-            d.tv_brow = upload_array(tv_brow, st, "upload tile entries");
+            // 1- and 3-row tiles carry the B rows in their value records.
+            if (!vcsr::tile_dev_folds_brow(tv.R))
+                d.tv_brow = upload_array(tv_brow, st, "upload tile entries");
             d.tv_val = upload_array(vcsr::tile_dev_folds_brow(tv.R) ? tv_val : tv.val, st,
                                     "upload tile values");
             d.tv_mask = upload_array(tv.mask, st, "upload tile masks");

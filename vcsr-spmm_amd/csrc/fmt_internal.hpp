@@ -42,6 +42,7 @@ struct DeviceFmt {
     int32_t tv_n_chunks = 0;
     int32_t* tv_pieces = nullptr;       // 4 per piece: row, rows, first entry, partial row
     int32_t* tv_brow = nullptr;         // per entry: B row, kTileNoEntry for placeholders
+                                        // (not uploaded for 1- and 3-row tiles)
     float* tv_val = nullptr;            // tile_dev_stride per entry: values (0 where absent),
                                         // then the B row's bits for 1- and 3-row tiles
     uint16_t* tv_mask = nullptr;        // per entry: presence bit per tile row
