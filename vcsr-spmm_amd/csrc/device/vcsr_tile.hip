@@ -52,7 +52,9 @@
 namespace vcsr {
 namespace {
 
-constexpr int kWaves = 4;
+// Waves per block of the VALU tile kernel: 2 (1.5% faster than 4 on the
+// banded matrix — a freed wave slot waits less for a whole block to fit).
+constexpr int kWaves = 2;
 // Buffer offset of "no B row": at least 2^31, above any buffer-path B size,
 // and still below 2^32 after adding a column offset (< 2^31).
 constexpr uint32_t kNoRow = 0x80000000u;
