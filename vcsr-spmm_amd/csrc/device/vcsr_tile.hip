@@ -672,14 +672,16 @@ void launch_mma_buf(const DeviceFmt& d, dim3 grid, int64_t waves, int32_t n_ct, 
     // Measured on the 16K block-sparse matrix (1,024 tiles): O = 32 / 64,
     // one wave per SIMD, 4 groups with the barrier 27% / 36% faster; O = 128
     // / 192, two or three, 2 groups with the barrier 20% / 4% faster; O >= 256
-    // slower with the barrier (O = 512: 236 / 186 against 152 us).
+    // slower with the barrier (O = 512: 236 / 186 against 152 us).  Without
+    // it the compiler interleaves loads and MFMAs whatever the block size (42
+    // VGPRs); 8 groups measured 1-4% faster than 4 at O = 256 / 512.
     const int64_t simds = 4 * (int64_t)device_cus(d.device);
     if (waves <= simds)
         launch_mma_as<VEC, BUF, 4, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
     else if (waves <= 3 * simds)
         launch_mma_as<VEC, BUF, 2, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
     else
-        launch_mma_as<VEC, BUF, 4, false>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
+        launch_mma_as<VEC, BUF, 8, false>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
 }
 
 template <int VEC>
