@@ -486,7 +486,8 @@ def run_csr_wave_spmm_gpu(M, N, d_rowptr, d_col, d_val, dB, O, dC, stream=None, 
 
 
 def run_vcsr_spmm_gpu(fmt: Vcsr, dB, O, tileK, dC, stream=None, timed=False):
-    """C += A*B with the segmented-streaming kernel; zero C first."""
+    """C += A*B (spmm_vcsr: the default kernel, the reference's accumulate
+    semantics, so zero C first)."""
     ms = C.c_float(0)
     _check(load_library().spmm_vcsr(fmt._h, dB.ptr, O, tileK, dC.ptr, _sp(stream),
                                     C.byref(ms) if timed else None))
