@@ -81,17 +81,61 @@ def measured_traffic(config, algo):
         return None
 
 
-def cpu_baseline(orc, csr, B, seconds):
-    """The oracle's single-thread FP32 CSR SpMM (reference loop order) on the
-    same matrix and B, repeated until `seconds` of CPU work."""
+def host_threads():
+    """Threads the CPU baseline may use: the cores this process may run on,
+    at most 16 (one GPU's share of the GPU box's host) and at most
+    OMP_NUM_THREADS when that is set."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, min(n, 16))
+
+
+def host_description():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": aff}
+
+
+def cpu_baseline(orc, csr, B, seconds, nthreads):
+    """The oracle's FP32 CSR SpMM (reference loop order, rows split over
+    `nthreads` threads) on the same matrix and B, repeated until `seconds`
+    of wall time after one untimed warm-up run.  Returns (GFLOP/s, reps,
+    seconds, median seconds per SpMM)."""
     flop = 2.0 * csr.nnz * B.shape[1]
-    reps, t_total = 0, 0.0
-    while t_total < seconds and reps < 1000:
+    orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B, nthreads)
+    times = []
+    while sum(times) < seconds and len(times) < 1000:
         t0 = time.perf_counter()
-        orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
-        t_total += time.perf_counter() - t0
-        reps += 1
-    return flop * reps / t_total / 1e9, reps, t_total
+        orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B, nthreads)
+        times.append(time.perf_counter() - t0)
+    t_total = sum(times)
+    return flop * len(times) / t_total / 1e9, len(times), t_total, float(np.median(times))
+
+
+def full_check(orc, csr, B, C, nthreads):
+    """Every element of C against the oracle's double-accumulated CSR SpMM:
+    north-star relative L2 error <= 1e-5 and, per row r, max-abs error <=
+    1e-4 * ||A_r||_1 * max|B|.  Returns (rel_l2, worst max-abs / bound)."""
+    ref = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B, nthreads)
+    diff = C.astype(np.float64) - ref
+    rel = float(np.linalg.norm(diff) / max(np.linalg.norm(ref), 1e-300))
+    row_l1 = np.bincount(np.repeat(np.arange(csr.M), np.diff(csr.row_ptr)),
+                         weights=np.abs(csr.val.astype(np.float64)), minlength=csr.M)
+    bound = 1e-4 * row_l1 * float(np.abs(B).max() if B.size else 0.0)
+    err = np.abs(diff).max(axis=1) if diff.size else np.zeros(csr.M)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ratio = np.where(bound > 0, err / bound, np.where(err > 0, np.inf, 0.0))
+    return rel, float(ratio.max() if ratio.size else 0.0)
 
 
 def main():
@@ -106,7 +150,8 @@ def main():
     ap.add_argument("--tileK", type=int, default=None)
     ap.add_argument("--cols", type=int, default=None, metavar="O",
                     help="columns of B and C instead of the config's O")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="wall seconds of each CPU baseline mode (1 thread, all threads)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only copy a BYTES buffer device-to-device --steps times (the "
@@ -229,16 +274,23 @@ def main():
     lib.vcsr_device_sync()
     C = dC.numpy(st)
 
-    # Correctness of the last step: sampled rows against the oracle (double).
-    rng = np.random.default_rng(0)
-    rows = np.unique(rng.choice(csr.M, size=min(512, csr.M), replace=False))
-    rp = np.concatenate([[0], np.cumsum(np.diff(csr.row_ptr)[rows])]).astype(np.int32)
-    cols = np.concatenate([csr.col[csr.row_ptr[r]:csr.row_ptr[r + 1]] for r in rows])
-    vals = np.concatenate([csr.val[csr.row_ptr[r]:csr.row_ptr[r + 1]] for r in rows])
-    ref = orc.spmm_f64(len(rows), rp, cols.astype(np.int32), vals.astype(np.float32), B)
-    rel = float(np.linalg.norm(C[rows] - ref) / max(np.linalg.norm(ref), 1e-300))
-    check = "pass" if rel <= 1e-5 else "FAIL"
-    log(f"bench: sampled-row rel L2 vs oracle {rel:.2e} ({check})")
+    # Per-step durations for the median: a second pass of K steps with an
+    # event between consecutive steps (the headline uses the first pass).
+    evs = [vs.Event() for _ in range(args.steps + 1)]
+    lib.vcsr_device_sync()
+    evs[0].record(st)
+    for i in range(args.steps):
+        step()
+        evs[i + 1].record(st)
+    step_ms = [evs[i].elapsed_ms(evs[i + 1]) for i in range(args.steps)]
+    lib.vcsr_device_sync()
+
+    # Correctness of the last step of the first pass: every element of C
+    # against the oracle (double), the north-star bounds.
+    nthreads = host_threads()
+    rel, worst = full_check(orc, csr, B, C, nthreads)
+    check = "pass" if rel <= 1e-5 and worst <= 1.0 else "FAIL"
+    log(f"bench: whole-C check vs oracle: rel L2 {rel:.2e}, max-abs / bound {worst:.3f} ({check})")
 
     # Kernel-only duration: the kernel alone, K launches back to back between
     # two events on the stream it runs on (C is left accumulating; the
@@ -269,6 +321,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step_median": round(float(np.median(step_ms)), 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -282,7 +335,8 @@ def main():
                    else "SpMM kernel writing C = A*B"},
         "kernel_ms": round(kernel_ms, 5),
         "kernel_gflops": round(flop / (kernel_ms * 1e-3) / 1e9, 2),
-        "check": {"rel_l2_sampled_rows": rel, "result": check},
+        "check": {"rows": "all", "rel_l2": rel, "maxabs_over_bound": round(worst, 4),
+                  "result": check},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": (measured_traffic(args.config, args.algo)
@@ -309,12 +363,23 @@ def main():
                            "frac": round(useful / MFMA_FP32_PEAK_TFS, 4),
                            "traffic": out["roofline"]["traffic"], "bytes_alg": bytes_alg}
     if not args.no_cpu_baseline:
-        gf, reps, secs = cpu_baseline(orc, csr, B, args.cpu_seconds)
-        out["cpu_baseline"] = {"value": round(gf, 3), "unit": "GFLOP/s", "cores": 1,
-                               "kind": "port",
-                               "sample": f"full {args.config} matrix x B (O={O}), {reps} reps, "
-                                         f"{secs:.1f}s, oracle FP32 CSR SpMM single thread"}
+        # The oracle's FP32 CSR SpMM (the reference's loop order; the
+        # reference has no CPU SpMM of its own) on the same matrix and B:
+        # all of this process's host threads (value), and one thread.
+        gf, reps, secs, med = cpu_baseline(orc, csr, B, args.cpu_seconds, nthreads)
+        gf1, reps1, secs1, med1 = cpu_baseline(orc, csr, B, args.cpu_seconds, 1)
+        out["cpu_baseline"] = {
+            "value": round(gf, 3), "unit": "GFLOP/s", "cores": nthreads, "kind": "port",
+            "sample": f"full {args.config} matrix x B (O={O}), {reps} SpMMs in {secs:.1f}s "
+                      f"(median {med * 1e3:.1f} ms), oracle FP32 CSR SpMM, rows split over "
+                      f"{nthreads} threads",
+            "single_thread": {"value": round(gf1, 3), "cores": 1,
+                              "sample": f"{reps1} SpMMs in {secs1:.1f}s (median "
+                                        f"{med1 * 1e3:.1f} ms)"},
+            "host": host_description()}
     print(json.dumps(out), flush=True)
+    if check != "pass":
+        sys.exit(1)
 
 
 if __name__ == "__main__":

@@ -84,6 +84,10 @@ def oracle_lib():
         lib.orc_spmm_f32.restype = None
         lib.orc_spmm_f64.argtypes = lib.orc_spmm_f32.argtypes
         lib.orc_spmm_f64.restype = None
+        lib.orc_spmm_f32_mt.argtypes = lib.orc_spmm_f32.argtypes + [C.c_int]
+        lib.orc_spmm_f32_mt.restype = None
+        lib.orc_spmm_f64_mt.argtypes = lib.orc_spmm_f32_mt.argtypes
+        lib.orc_spmm_f64_mt.restype = None
         lib.orc_vcsr_apply.argtypes = [C.c_int] * 5 + [C.c_void_p] * 7 + [C.c_int, C.c_void_p]
         lib.orc_vcsr_apply.restype = None
         _orc = lib
@@ -165,24 +169,29 @@ def build(M, N, row_ptr, col, val, segw, bundle, layout):
     return _fmt_dict(lib.orc_free, f, True)
 
 
-def spmm_f32(M, row_ptr, col, val, B):
+def _spmm(M, row_ptr, col, val, B, dtype, nthreads):
     lib = oracle_lib()
     B = np.ascontiguousarray(B, np.float32)
-    out = np.empty((M, B.shape[1]), np.float32)
-    lib.orc_spmm_f32(M, _p(np.ascontiguousarray(row_ptr, np.int32)),
-                     _p(np.ascontiguousarray(col, np.int32)),
-                     _p(np.ascontiguousarray(val, np.float32)), _p(B), B.shape[1], _p(out))
+    out = np.empty((M, B.shape[1]), dtype)
+    args = (M, _p(np.ascontiguousarray(row_ptr, np.int32)), _p(np.ascontiguousarray(col, np.int32)),
+            _p(np.ascontiguousarray(val, np.float32)), _p(B), B.shape[1], _p(out))
+    f32 = dtype == np.float32
+    if nthreads == 1:
+        (lib.orc_spmm_f32 if f32 else lib.orc_spmm_f64)(*args)
+    else:
+        (lib.orc_spmm_f32_mt if f32 else lib.orc_spmm_f64_mt)(*args, int(nthreads))
     return out
 
 
-def spmm_f64(M, row_ptr, col, val, B):
-    lib = oracle_lib()
-    B = np.ascontiguousarray(B, np.float32)
-    out = np.empty((M, B.shape[1]), np.float64)
-    lib.orc_spmm_f64(M, _p(np.ascontiguousarray(row_ptr, np.int32)),
-                     _p(np.ascontiguousarray(col, np.int32)),
-                     _p(np.ascontiguousarray(val, np.float32)), _p(B), B.shape[1], _p(out))
-    return out
+def spmm_f32(M, row_ptr, col, val, B, nthreads=1):
+    """FP32 CSR SpMM in the reference loop order; nthreads != 1 splits the
+    rows over threads (<= 0: all hardware threads), same result."""
+    return _spmm(M, row_ptr, col, val, B, np.float32, nthreads)
+
+
+def spmm_f64(M, row_ptr, col, val, B, nthreads=1):
+    """The same sum accumulated in double (the tolerance checks' reference)."""
+    return _spmm(M, row_ptr, col, val, B, np.float64, nthreads)
 
 
 def vcsr_apply(M, N, fmt, B):

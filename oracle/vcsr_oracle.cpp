@@ -13,6 +13,8 @@
 //   orc_build_tc         src/vcsr_tc.cu:26-106        (layout S with segw=16, bundle=16)
 //   orc_spmm_f32         src/kernels.cu:25-32 loop order (row; p ascending; k inner; FMA)
 //   orc_spmm_f64         same sum in double (checker only)
+//   orc_spmm_f{32,64}_mt the same two over row ranges on several threads
+//                        (rows are independent: bit-identical results)
 //   orc_vcsr_apply       src/vcsr_seg.cu:173-188 semantics (C += per-group partial
 //                        sums) evaluated in double, to check that a format
 //                        represents A
@@ -28,6 +30,7 @@
 #include <sstream>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -374,6 +377,38 @@ void orc_spmm_f64(int M, const int* row_ptr, const int* col, const float* val, c
             for (int k = 0; k < O; ++k) c[k] += a * (double)b[k];
         }
     }
+}
+
+// The two sums above over contiguous row ranges on `nthreads` threads (<= 0:
+// every hardware thread).  Rows are independent, so each row's result is the
+// single-thread one bit for bit; only the wall time changes (the all-cores
+// CPU baseline, and whole-C checks of large products).
+extern "C++" {
+template <class T, class F>
+static void rows_in_parallel(int M, const int* row_ptr, int O, T* C, int nthreads, F one) {
+    int nt = nthreads > 0 ? nthreads : (int)std::thread::hardware_concurrency();
+    nt = std::max(1, std::min(nt, std::max(M, 1)));
+    std::vector<std::thread> th;
+    for (int t = 0; t < nt; ++t) {
+        const int r0 = (int)((int64_t)M * t / nt), r1 = (int)((int64_t)M * (t + 1) / nt);
+        th.emplace_back([=] { one(r1 - r0, row_ptr + r0, C + (size_t)r0 * O); });
+    }
+    for (auto& x : th) x.join();
+}
+}  // extern "C++"
+
+void orc_spmm_f32_mt(int M, const int* row_ptr, const int* col, const float* val, const float* B,
+                     int O, float* C, int nthreads) {
+    rows_in_parallel(M, row_ptr, O, C, nthreads, [=](int m, const int* rp, float* c) {
+        orc_spmm_f32(m, rp, col, val, B, O, c);
+    });
+}
+
+void orc_spmm_f64_mt(int M, const int* row_ptr, const int* col, const float* val, const float* B,
+                     int O, double* C, int nthreads) {
+    rows_in_parallel(M, row_ptr, O, C, nthreads, [=](int m, const int* rp, double* c) {
+        orc_spmm_f64(m, rp, col, val, B, O, c);
+    });
 }
 
 // C += A_fmt * B in double, walking the packed format the way the reference

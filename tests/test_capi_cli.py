@@ -62,6 +62,44 @@ def test_gpu_entry_points_without_gpu(vs):
     assert rc == vs.VCSR_EINVAL
 
 
+class _FakeBuf:
+    """Stands in for a device buffer: the Python layer checks shape and type
+    before it hands a pointer to the library."""
+
+    def __init__(self, n, dtype=np.float32):
+        self.dtype, self.nbytes, self.ptr = np.dtype(dtype), n * np.dtype(dtype).itemsize, None
+
+
+def test_python_wrappers_check_buffer_sizes(vs):
+    """B and C must hold N*O and M*O float32 elements, and CSR arrays must
+    be int32/float32 of matching lengths: a short or mistyped buffer is
+    VCSR_EINVAL in Python, before the library (and a kernel) sees it."""
+    csr = vs.coo_to_csr(vs.generate_coo(1, 0))
+    fmt = vs.csr_to_vcsr_seg(csr, 4, 64)
+    M, N, O = csr.M, csr.N, 32
+    good_b, good_c = _FakeBuf(N * O), _FakeBuf(M * O)
+    calls = [
+        lambda b, c: vs.run_vcsr_spmm_gpu(fmt, b, O, 64, c),
+        lambda b, c: vs.run_vcsr_spmm_gpu_ex(fmt, b, O, 64, c, kernel=vs.KERNEL_TILE),
+        lambda b, c: vs.run_vcsr_tc_spmm_gpu(fmt, b, O, c),
+    ]
+    for call in calls:
+        for b, c in ((_FakeBuf(N * O - 1), good_c), (good_b, _FakeBuf(M * O - 4)),
+                     (_FakeBuf(N * O, np.float64), good_c), (good_b, _FakeBuf(M * O, np.int32))):
+            with pytest.raises(vs.VcsrError) as e:
+                call(b, c)
+            assert e.value.code == vs.VCSR_EINVAL
+    rp, col, val = _FakeBuf(M + 1, np.int32), _FakeBuf(csr.nnz, np.int32), _FakeBuf(csr.nnz)
+    for args in ((_FakeBuf(M, np.int32), col, val), (rp, _FakeBuf(csr.nnz), val),
+                 (rp, col, _FakeBuf(csr.nnz - 1))):
+        for run in (lambda a: vs.run_csr_spmm_gpu(M, *a, good_b, O, good_c),
+                    lambda a: vs.run_csr_wave_spmm_gpu(M, N, *a, good_b, O, good_c),
+                    lambda a: vs.run_vendor_spmm_gpu(M, N, csr.nnz, *a, good_b, O, good_c)):
+            with pytest.raises(vs.VcsrError) as e:
+                run(args)
+            assert e.value.code == vs.VCSR_EINVAL
+
+
 def run_cli(vs, *args):
     return subprocess.run([vs.CLI_PATH, *args], capture_output=True, text=True, timeout=300)
 

@@ -562,7 +562,7 @@ class _Shifted:
         import ctypes
         self._lib = vs.load_library()
         self._st = st
-        self.shape, self.nbytes = a.shape, a.nbytes
+        self.shape, self.nbytes, self.dtype = a.shape, a.nbytes, a.dtype
         self._base = vs.DeviceArray((a.nbytes + 64,), np.uint8)
         self.ptr = ctypes.c_void_p(self._base.ptr.value + off)
         a = np.ascontiguousarray(a)

@@ -369,9 +369,30 @@ def test_format_file_rejects_bad_files(vs, tmp_path):
     with_int(base0, 4, "segment_base")            # group 0 sits in segment 0
     with_int(rows0, csr.M, "row_out_of_range")
     with_int(lcol0, 4, "lcol_out_of_segment")     # segw = 4
+    # Valid arrays under a bad row-tile setting in the header.
+    with_int(8 + 24, 5, "tile_height_5")
+    with_int(8 + 28, 2, "window_flag_2")
     # An entry after a padding slot of the same lane.
     a = fmt.arrays()
     pad = int(np.nonzero(a["lcol"] < 0)[0][0])
     with_int(lcol0 + 4 * pad, 0, "unpacked_lane")
+    # A self-consistent file whose one group has depth 0 (no slots at all):
+    # the builders never emit such a group, and the upload reads every
+    # group's depth-0 slots.
+    zero = bytearray(data[:8])
+    zero += np.array([1, 1, 1, 1, vs.LAYOUT_S, 1, 0, 0], np.int32).tobytes()
+    zero += np.array([1, 0], np.int64).tobytes()                 # G = 1, P = 0
+    zero += np.array([0, 0, 0, 0, 0], np.int32).tobytes()        # ptr, depth, base, rows
+    zero += np.array([0, 1], np.int32).tobytes()                 # segment_group_start
+    expect(zero, vs.VCSR_EINVAL, "zero_depth")
+    ok = bytearray(data[:8])                                     # the same with depth 1
+    ok += np.array([1, 1, 1, 1, vs.LAYOUT_S, 1, 0, 0], np.int32).tobytes()
+    ok += np.array([1, 1], np.int64).tobytes()
+    ok += np.array([0, 1, 1, 0, 0], np.int32).tobytes()
+    ok += np.array([0], np.int32).tobytes() + np.array([2.5], np.float32).tobytes()
+    ok += np.array([0, 1], np.int32).tobytes()
+    p = tmp_path / "one.vcsr"
+    p.write_bytes(bytes(ok))
+    assert vs.load_vcsr(str(p)).num_groups == 1
     # The untouched file still loads.
     assert vs.load_vcsr(str(good)).num_groups == G

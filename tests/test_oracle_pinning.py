@@ -266,3 +266,21 @@ def test_spmm_dense_reference(orc):
     assert np.allclose(C64, ref, rtol=1e-13, atol=1e-13)
     C32 = orc.spmm_f32(M, rp, col, val, B)
     assert np.linalg.norm(C32 - ref) <= 1e-6 * np.linalg.norm(ref)
+
+
+@pytest.mark.parametrize("nthreads", [2, 3, 7, 0])
+def test_threaded_spmm_is_the_single_thread_result(orc, nthreads):
+    """The row-split oracle SpMM (all-cores CPU baseline, whole-C checks)
+    gives the single-thread result bit for bit, in FP32 and in double,
+    including empty rows, duplicates and more threads than rows."""
+    rng = np.random.default_rng(40 + nthreads)
+    for M, N, O in ((300, 200, 17), (5, 9, 3), (0, 4, 2)):
+        rows, cols, vals = random_csr(rng, M, N, density=0.1, dup_rate=0.1, empty_rows=0.2)
+        rp, col, val = orc.coo_to_csr(M, N, rows, cols, vals)
+        B = rng.uniform(-1, 1, size=(N, O)).astype(np.float32)
+        one32 = orc.spmm_f32(M, rp, col, val, B)
+        one64 = orc.spmm_f64(M, rp, col, val, B)
+        assert np.array_equal(orc.spmm_f32(M, rp, col, val, B, nthreads).view(np.uint32),
+                              one32.view(np.uint32))
+        assert np.array_equal(orc.spmm_f64(M, rp, col, val, B, nthreads).view(np.uint64),
+                              one64.view(np.uint64))

@@ -433,8 +433,39 @@ class DeviceArray:
             self.ptr = C.c_void_p()
 
 
+def _need_buf(arr, dtype, count, what):
+    """Raises VcsrError(VCSR_EINVAL) unless the device buffer `arr` holds at
+    least `count` elements of `dtype`: the kernels index B and C by the
+    shapes they are given, so a short or mistyped buffer would be read or
+    written past its end on the device."""
+    want = np.dtype(dtype)
+    have = getattr(arr, "dtype", want)
+    if np.dtype(have) != want:
+        raise VcsrError(VCSR_EINVAL, f"{what}: dtype {np.dtype(have)}, expected {want}")
+    nbytes = getattr(arr, "nbytes", None)
+    if nbytes is None or int(nbytes) < int(count) * want.itemsize:
+        raise VcsrError(VCSR_EINVAL, f"{what}: {nbytes} bytes, need {int(count) * want.itemsize}")
+
+
+def _need_csr(M, d_rowptr, d_col, d_val):
+    _need_buf(d_rowptr, np.int32, M + 1, "row_ptr")
+    _need_buf(d_col, np.int32, 0, "col")
+    _need_buf(d_val, np.float32, 0, "val")
+    if d_col.nbytes // 4 != d_val.nbytes // 4:
+        raise VcsrError(VCSR_EINVAL, "col and val lengths differ")
+
+
+def _need_bc(N, M, O, dB, dC):
+    if O < 0:
+        raise VcsrError(VCSR_EINVAL, "negative O")
+    _need_buf(dB, np.float32, N * O, "B")
+    _need_buf(dC, np.float32, M * O, "C")
+
+
 def run_csr_spmm_gpu(M, d_rowptr, d_col, d_val, dB, O, dC, stream=None, timed=False):
     """C = A*B (overwrites C).  Returns kernel ms when timed (synchronous)."""
+    _need_csr(M, d_rowptr, d_col, d_val)
+    _need_bc(0, M, O, dB, dC)
     ms = C.c_float(0)
     _check(load_library().spmm_csr_naive(M, d_rowptr.ptr, d_col.ptr, d_val.ptr, dB.ptr, O,
                                          dC.ptr, _sp(stream), C.byref(ms) if timed else None))
@@ -447,6 +478,8 @@ class VendorPlan:
     with its set-up done once."""
 
     def __init__(self, M, N, nnz, d_rowptr, d_col, d_val, dB, O, dC, stream=None):
+        _need_csr(M, d_rowptr, d_col, d_val)
+        _need_bc(N, M, O, dB, dC)
         h = C.c_void_p()
         _check(load_library().vcsr_vendor_plan_create(M, N, nnz, d_rowptr.ptr, d_col.ptr,
                                                       d_val.ptr, dB.ptr, O, dC.ptr, _sp(stream),
@@ -470,6 +503,8 @@ class VendorPlan:
 def run_vendor_spmm_gpu(M, N, nnz, d_rowptr, d_col, d_val, dB, O, dC, stream=None, timed=False):
     """One-shot rocSPARSE C = A*B (set-up, SpMM, tear-down, like the
     reference's cuSPARSE wrapper); the SpMM call's ms when timed."""
+    _need_csr(M, d_rowptr, d_col, d_val)
+    _need_bc(N, M, O, dB, dC)
     ms = C.c_float(0)
     _check(load_library().spmm_csr_vendor(M, N, nnz, d_rowptr.ptr, d_col.ptr, d_val.ptr, dB.ptr,
                                           O, dC.ptr, _sp(stream), C.byref(ms) if timed else None))
@@ -479,6 +514,8 @@ def run_vendor_spmm_gpu(M, N, nnz, d_rowptr, d_col, d_val, dB, O, dC, stream=Non
 def run_csr_wave_spmm_gpu(M, N, d_rowptr, d_col, d_val, dB, O, dC, stream=None, timed=False):
     """C = A*B with the wave-per-row CSR kernel (overwrites C); kernel ms
     when timed (synchronous)."""
+    _need_csr(M, d_rowptr, d_col, d_val)
+    _need_bc(N, M, O, dB, dC)
     ms = C.c_float(0)
     _check(load_library().spmm_csr_wave(M, N, d_rowptr.ptr, d_col.ptr, d_val.ptr, dB.ptr, O,
                                         dC.ptr, _sp(stream), C.byref(ms) if timed else None))
@@ -488,6 +525,7 @@ def run_csr_wave_spmm_gpu(M, N, d_rowptr, d_col, d_val, dB, O, dC, stream=None, 
 def run_vcsr_spmm_gpu(fmt: Vcsr, dB, O, tileK, dC, stream=None, timed=False):
     """C += A*B (spmm_vcsr: the default kernel, the reference's accumulate
     semantics, so zero C first)."""
+    _need_bc(fmt.N, fmt.M, O, dB, dC)
     ms = C.c_float(0)
     _check(load_library().spmm_vcsr(fmt._h, dB.ptr, O, tileK, dC.ptr, _sp(stream),
                                     C.byref(ms) if timed else None))
@@ -496,6 +534,7 @@ def run_vcsr_spmm_gpu(fmt: Vcsr, dB, O, tileK, dC, stream=None, timed=False):
 
 def run_vcsr_tc_spmm_gpu(fmt: Vcsr, dB, O, dC, stream=None, timed=False):
     """C += A*B with the FP32-MFMA dense-tile kernel; zero C first."""
+    _need_bc(fmt.N, fmt.M, O, dB, dC)
     ms = C.c_float(0)
     _check(load_library().spmm_vcsr_mfma(fmt._h, dB.ptr, O, dC.ptr, _sp(stream),
                                          C.byref(ms) if timed else None))
@@ -525,6 +564,7 @@ def tile_mfma_work(fmt: Vcsr, O: int) -> tuple[int, int]:
 def run_vcsr_spmm_gpu_ex(fmt: Vcsr, dB, O, tileK, dC, stream=None, timed=False,
                          kernel=KERNEL_AUTO, accumulate=True):
     """SpMM with an explicit kernel; accumulate=False computes C = A*B."""
+    _need_bc(fmt.N, fmt.M, O, dB, dC)
     ms = C.c_float(0)
     _check(load_library().spmm_vcsr_ex(fmt._h, dB.ptr, O, tileK, dC.ptr, _sp(stream),
                                        C.byref(ms) if timed else None, kernel,

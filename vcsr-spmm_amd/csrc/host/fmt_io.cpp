@@ -65,7 +65,10 @@ void validate_vcsr(const Vcsr& v) {
     if (v.group_ptr[0] != 0) bad("group_ptr[0] != 0");
     for (int64_t g = 0; g < G; ++g) {
         const int64_t d = v.group_depth[(size_t)g];
-        if (d < 0) bad("negative depth");
+        // Every builder emits groups of depth >= 1 (layout H skips all-empty
+        // bundles, layouts S and TC group active rows only), and the upload
+        // reads each group's depth-0 slots.
+        if (d < 1) bad("group depth below 1");
         if ((int64_t)v.group_ptr[(size_t)g + 1] - v.group_ptr[(size_t)g] != d * b)
             bad("group_ptr does not advance by depth * bundle");
     }
