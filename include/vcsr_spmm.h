@@ -230,6 +230,21 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
                  float* dC, void* stream, float* ms, int32_t kernel,
                  int32_t accumulate);
 
+/* The default kernel (VCSR_KERNEL_TILE, as spmm_vcsr_ex runs it) without any
+ * device allocation in the call, for callers that cannot allocate: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  No counterpart in the reference.  accumulate as in
+ * spmm_vcsr_ex (0: C = A*B, 1: C += A*B).  Enqueued on `stream`, not waited
+ * for, no timing.  The partial rows of split tiles live in a fixed device
+ * array of 16 MiB (4 Mi floats) that each GPU holds until the process ends;
+ * a format and O that need more fail with VCSR_ERANGE before any launch
+ * (spmm_vcsr_ex has no such limit).  Every call on one GPU uses that GPU's
+ * array, so calls that overlap in time on one GPU race; its contents are
+ * written before they are read, so a call never sees an earlier one's.
+ * The format must be uploaded to the current device. */
+int spmm_vcsr_noalloc(const vcsr_fmt* fmt, const float* dB, int32_t O, float* dC,
+                      void* stream, int32_t accumulate);
+
 /* C += A*B on FP32 MFMA: every group is collapsed to a dense bundle x segw
  * tile and multiplied by the segment's B tile on the matrix cores (FP32 in,
  * FP32 accumulate).  Meant for dense sub-blocks (layout TC); valid for any

@@ -1,0 +1,92 @@
+"""spmm_vcsr_noalloc (the default kernel with its split-tile scratch in the
+library's fixed per-device array instead of allocated memory) against
+spmm_vcsr_ex with the same kernel, through the C ABI: two calls in a row,
+the second on a smaller input, both C modes; a format whose split tiles
+need more than the array holds is refused before any launch."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _long_row_csr(vs, seed, M, N, every, long_len, short_len):
+    """Rows of short_len uniform columns, every `every`-th row long_len:
+    the long rows' 1-row tiles are cut into pieces that write partial rows
+    (the scratch), summed by the reduce kernel."""
+    rng = np.random.default_rng(seed)
+    lens = np.where(np.arange(M) % every == 3, long_len, short_len)
+    rows = np.repeat(np.arange(M, dtype=np.int32), lens)
+    cols = np.concatenate([rng.choice(N, size=n, replace=False) for n in lens]).astype(np.int32)
+    vals = rng.uniform(-1, 1, size=rows.size).astype(np.float32)
+    return vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
+
+
+def _both(vs, st, csr, O, accumulate, seed):
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.upload(st)
+    B = vs.gen_dense(seed, 0, csr.N, O)
+    C0 = vs.gen_dense(seed + 1, 0, csr.M, O)
+    dB = vs.DeviceArray.from_numpy(B, st)
+    d_ref = vs.DeviceArray.from_numpy(C0, st)
+    d_got = vs.DeviceArray.from_numpy(C0, st)
+    vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, 64, d_ref, st, kernel=vs.KERNEL_TILE,
+                            accumulate=accumulate)
+    vs.run_vcsr_spmm_gpu_noalloc(fmt, dB, O, d_got, st, accumulate=accumulate)
+    st.sync()
+    return fmt, B, C0, d_ref.numpy(st), d_got.numpy(st)
+
+
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_noalloc_matches_the_allocating_entry_point(gpu, orc, accumulate):
+    vs = gpu
+    st = vs.Stream()
+    print(f"noalloc: call 1, 600 rows with split tiles, O=200, accumulate={accumulate}", flush=True)
+    big = _long_row_csr(vs, 11, 600, 60000, 20, 2500, 16)
+    fmt, B, C0, ref, got = _both(vs, st, big, 200, accumulate, 21)
+    assert fmt.tile_info()[0] == 1
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # The result is the product (not only the same as the other entry point).
+    want = orc.spmm_f64(big.M, big.row_ptr, big.col, big.val, B)
+    if accumulate:
+        want = want + C0.astype(np.float64)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel <= 1e-5, rel
+    print(f"noalloc: call 2, 90 rows, O=64, accumulate={accumulate}", flush=True)
+    small = _long_row_csr(vs, 12, 90, 9000, 7, 700, 5)
+    _, B2, C02, ref2, got2 = _both(vs, st, small, 64, accumulate, 31)
+    assert np.array_equal(got2.view(np.uint32), ref2.view(np.uint32))
+    want2 = orc.spmm_f64(small.M, small.row_ptr, small.col, small.val, B2)
+    if accumulate:
+        want2 = want2 + C02.astype(np.float64)
+    assert np.linalg.norm(got2 - want2) <= 1e-5 * np.linalg.norm(want2)
+
+
+def test_noalloc_refuses_more_scratch_than_it_holds(gpu):
+    """300 rows of 3,600 columns at O = 256: 17,100 partial rows of 256
+    floats (4.38 Mi floats) exceed the 4 Mi-float array: VCSR_ERANGE, C
+    untouched; spmm_vcsr_ex (which allocates) still computes it."""
+    vs = gpu
+    st = vs.Stream()
+    csr = _long_row_csr(vs, 13, 300, 100000, 1, 3600, 3600)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.upload(st)
+    O = 256
+    dB = vs.DeviceArray.from_numpy(vs.gen_dense(41, 0, csr.N, O), st)
+    dC = vs.DeviceArray((csr.M, O), np.float32)
+    dC.zero(st)
+    with pytest.raises(vs.VcsrError) as e:
+        vs.run_vcsr_spmm_gpu_noalloc(fmt, dB, O, dC, st)
+    assert e.value.code == vs.VCSR_ERANGE
+    assert "scratch" in str(e.value)
+    st.sync()
+    assert not dC.numpy(st).any()
+    vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, 64, dC, st, kernel=vs.KERNEL_TILE, accumulate=False)
+    st.sync()
+    assert np.isfinite(dC.numpy(st)).all() and dC.numpy(st).any()
+    # A null format is refused the same way as by the other entry points.
+    lib = vs.load_library()
+    assert lib.spmm_vcsr_noalloc(None, dB.ptr, O, dC.ptr, st.h, 0) == vs.VCSR_EINVAL

@@ -43,7 +43,7 @@ EXPORTS = (
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_save vcsr_fmt_load "
     "vcsr_fmt_upload "
     "vcsr_fmt_set_tile_rows vcsr_fmt_set_tile_windows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_csr_wave spmm_vcsr "
-    "spmm_vcsr_ex spmm_vcsr_mfma vcsr_mfma_work vcsr_tile_mfma_work spmm_csr_cpu "
+    "spmm_vcsr_ex spmm_vcsr_noalloc spmm_vcsr_mfma vcsr_mfma_work vcsr_tile_mfma_work spmm_csr_cpu "
     "vcsr_vendor_plan_create vcsr_vendor_spmm vcsr_vendor_plan_free spmm_csr_vendor "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
     "vcsr_memcpy_d2h vcsr_memcpy_d2d vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
@@ -119,6 +119,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "spmm_csr_wave": (C.c_int, [I32, I32, P, P, P, P, I32, P, P, pF]),
         "spmm_vcsr": (C.c_int, [P, P, I32, I32, P, P, pF]),
         "spmm_vcsr_ex": (C.c_int, [P, P, I32, I32, P, P, pF, I32, I32]),
+        "spmm_vcsr_noalloc": (C.c_int, [P, P, I32, P, P, I32]),
         "spmm_vcsr_mfma": (C.c_int, [P, P, I32, P, P, pF]),
         "vcsr_mfma_work": (C.c_int, [P, I32, I32, C.POINTER(I64), pI]),
         "vcsr_tile_mfma_work": (C.c_int, [P, I32, C.POINTER(I64), pI]),
@@ -570,3 +571,14 @@ def run_vcsr_spmm_gpu_ex(fmt: Vcsr, dB, O, tileK, dC, stream=None, timed=False,
                                        C.byref(ms) if timed else None, kernel,
                                        1 if accumulate else 0))
     return ms.value if timed else None
+
+
+def run_vcsr_spmm_gpu_noalloc(fmt: Vcsr, dB, O, dC, stream=None, accumulate=False):
+    """The default (tile-stationary) kernel through spmm_vcsr_noalloc: no
+    device allocation in the call; the partial rows of split tiles live in
+    the library's fixed 16 MiB per-device scratch array (VCSR_ERANGE beyond
+    it).  Enqueued only (not waited for); calls that overlap on one GPU race
+    on that scratch."""
+    _need_bc(fmt.N, fmt.M, O, dB, dC)
+    _check(load_library().spmm_vcsr_noalloc(fmt._h, dB.ptr, O, dC.ptr, _sp(stream),
+                                            1 if accumulate else 0))

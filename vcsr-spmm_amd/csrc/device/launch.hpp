@@ -48,9 +48,13 @@ hipError_t launch_vcsr_rowmajor(const Vcsr& v, const DeviceFmt& d, const float* 
 
 // vcsr_tile.hip: tile-stationary traversal of the VCSR slots through the
 // row-tile view; C = A*B (accumulate = 0) or C += A*B (accumulate = 1).
-// Needs d.partials sized for O when the view has split tiles.
+// `partials` holds the partial rows of split tiles: at least
+// tile_partials_floats(v, d, B, O, C) floats (none when the view has no
+// split tile); every partial row the launch reads it writes first.
 hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
-                            float* C, int32_t accumulate, hipStream_t st);
+                            float* C, int32_t accumulate, float* partials, hipStream_t st);
+int64_t tile_partials_floats(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                             const float* C);
 // MFMA instructions launch_vcsr_tile issues for one SpMM of width O when
 // the view has 16-row tiles (none otherwise), as launched for the alignment
 // of 16-byte aligned B and C.

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -112,6 +113,35 @@ RowView make_row_view(const vcsr::Vcsr& v, const std::vector<int32_t>& nact) {
         rv.split_rows.insert(rv.split_rows.end(), {r, first, rv.n_partials - first});
     }
     return rv;
+}
+
+// Scratch of spmm_vcsr_noalloc: the partial rows of split tiles, in a
+// file-scope device array instead of memory the call allocates.  Every GPU
+// the library runs on holds its own copy until the process ends.  In host
+// code `scratch` only names the symbol; its device address on the current
+// device comes from hipGetSymbolAddress (scratch_on_current_device), and
+// only that address is handed to kernels.
+constexpr size_t kScratchFloats = size_t(4) << 20;  // 16 MiB
+__device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of `scratch` on the current device, looked up once per device (on
+// the first call there, with that device current).
+float* scratch_on_current_device() {
+    int dev = -1;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) throw vcsr::Error(VCSR_EDEVICE, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (!p) throw vcsr::Error(VCSR_EDEVICE, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -285,7 +315,7 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
             if (kernel == VCSR_KERNEL_ROW)
                 return vcsr::launch_vcsr_rowmajor(fmt->v, d, dB, O, dC, accumulate, st);
             if (kernel == VCSR_KERNEL_TILE)
-                return vcsr::launch_vcsr_tile(fmt->v, d, dB, O, dC, accumulate, st);
+                return vcsr::launch_vcsr_tile(fmt->v, d, dB, O, dC, accumulate, d.partials, st);
             if (!accumulate && bytesC > 0) {
                 hipError_t e = hipMemsetAsync(dC, 0, bytesC, st);
                 if (e != hipSuccess) return e;
@@ -294,6 +324,34 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
                 return vcsr::launch_vcsr_stream(fmt->v, d, dB, O, tileK, dC, st);
             return vcsr::launch_vcsr_mfma(fmt->v, d, dB, O, tileK, dC, st);
         });
+    });
+}
+
+int spmm_vcsr_noalloc(const vcsr_fmt* fmt, const float* dB, int32_t O, float* dC, void* stream,
+                      int32_t accumulate) {
+    return guarded([&] {
+        need(fmt != nullptr, "null format");
+        need(O >= 0, "negative O");
+        need(accumulate == 0 || accumulate == 1, "accumulate must be 0 or 1");
+        if (!fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format not uploaded");
+        need(fmt->v.M == 0 || O == 0 || dC, "null C");
+        need(fmt->v.num_groups() == 0 || O == 0 || dB, "null B");
+        need_device();
+        const DeviceFmt& d = fmt->dev;
+        int dev = -1;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        if (dev != d.device)
+            throw vcsr::Error(VCSR_ESTATE, "format uploaded to another device than the current one");
+        float* sp = scratch_on_current_device();
+        const int64_t need_floats = vcsr::tile_partials_floats(fmt->v, d, dB, O, dC);
+        if (need_floats > (int64_t)kScratchFloats)
+            throw vcsr::Error(VCSR_ERANGE,
+                              "split tiles need " + std::to_string(need_floats) +
+                                  " floats of scratch at this O; the allocation-free entry point "
+                                  "holds " + std::to_string(kScratchFloats) +
+                                  " (16 MiB): use spmm_vcsr_ex");
+        hip_check(vcsr::launch_vcsr_tile(fmt->v, d, dB, O, dC, accumulate, sp, (hipStream_t)stream),
+                  "kernel launch");
     });
 }
 

@@ -654,18 +654,18 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
 
 template <int VEC, bool BUF, int GU, bool SB>
 void launch_mma_as(const DeviceFmt& d, dim3 grid, int32_t n_ct, int32_t O, int32_t accumulate,
-                   uint32_t b_bytes, const float* B, float* C, hipStream_t st) {
+                   uint32_t b_bytes, const float* B, float* C, float* partials, hipStream_t st) {
     hipLaunchKernelGGL((vcsr_tile_mma_kernel<VEC, BUF, GU, SB>), grid, dim3(64 * kMmaWaves), 0, st,
                        d.tv_n_chunks, n_ct, O, accumulate, b_bytes,
                        reinterpret_cast<const int4*>(d.tv_chunks),
                        reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask, d.tv_val,
-                       B, C, d.partials);
+                       B, C, partials);
 }
 
 template <int VEC, bool BUF>
 void launch_mma_buf(const DeviceFmt& d, dim3 grid, int64_t waves, int32_t n_ct, int32_t O,
                     int32_t accumulate, uint32_t b_bytes, const float* B, float* C,
-                    hipStream_t st) {
+                    float* partials, hipStream_t st) {
     // Few waves per SIMD (cfg5-like matrices at O <= 192): each wave's loads
     // in flight bound the time, so its loads go ahead of its MFMAs; with
     // many, 8 waves per SIMD with interleaved loads hide the latency better.
@@ -677,31 +677,32 @@ void launch_mma_buf(const DeviceFmt& d, dim3 grid, int64_t waves, int32_t n_ct, 
     // VGPRs); 8 groups measured 1-4% faster than 4 at O = 256 / 512.
     const int64_t simds = 4 * (int64_t)device_cus(d.device);
     if (waves <= simds)
-        launch_mma_as<VEC, BUF, 4, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
+        launch_mma_as<VEC, BUF, 4, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, partials, st);
     else if (waves <= 3 * simds)
-        launch_mma_as<VEC, BUF, 2, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
+        launch_mma_as<VEC, BUF, 2, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, partials, st);
     else
-        launch_mma_as<VEC, BUF, 8, false>(d, grid, n_ct, O, accumulate, b_bytes, B, C, st);
+        launch_mma_as<VEC, BUF, 8, false>(d, grid, n_ct, O, accumulate, b_bytes, B, C, partials,
+                                          st);
 }
 
 template <int VEC>
 hipError_t launch_mma(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, float* C,
-                      int32_t accumulate, hipStream_t st) {
+                      int32_t accumulate, float* partials, hipStream_t st) {
     const int32_t n_ct = (O + 16 * VEC - 1) / (16 * VEC);
     const int64_t waves = (int64_t)d.tv_n_chunks * n_ct;
     const dim3 grid((unsigned)((waves + kMmaWaves - 1) / kMmaWaves));
     const uint64_t b_bytes = (uint64_t)v.N * (uint64_t)O * 4u;
     if (b_bytes + 64u * 4u * (uint64_t)VEC >= kBufferLimit)
-        launch_mma_buf<VEC, false>(d, grid, waves, n_ct, O, accumulate, 0u, B, C, st);
+        launch_mma_buf<VEC, false>(d, grid, waves, n_ct, O, accumulate, 0u, B, C, partials, st);
     else
         launch_mma_buf<VEC, true>(d, grid, waves, n_ct, O, accumulate, (uint32_t)b_bytes, B, C,
-                                  st);
+                                  partials, st);
     return hipGetLastError();
 }
 
 template <int VEC, int LPE, int R, bool BUF>
 hipError_t launch_one(const DeviceFmt& d, const float* B, int32_t O, int32_t ld, float* C,
-                      int32_t accumulate, uint32_t b_bytes, hipStream_t st) {
+                      int32_t accumulate, uint32_t b_bytes, float* partials, hipStream_t st) {
     // Eight streams per wave (B slices of at most 8 columns) and single-row
     // tiles: four work items per wave, so each stream still gets several
     // rows.  Taller tiles stay one per wave (their streams split the tile's
@@ -712,47 +713,48 @@ hipError_t launch_one(const DeviceFmt& d, const float* B, int32_t O, int32_t ld,
     hipLaunchKernelGGL((vcsr_tile_kernel<VEC, LPE, R, MERGE, BUF>), grid, block, 0, st, d.tv_n_chunks, O,
                        ld, accumulate, b_bytes, reinterpret_cast<const int4*>(d.tv_chunks),
                        reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask, d.tv_val, B,
-                       C, d.partials);
+                       C, partials);
     return hipGetLastError();
 }
 
 template <int VEC, int R>
 hipError_t launch_r(const DeviceFmt& d, const float* B, int32_t O, int32_t ld, float* C,
-                    int32_t accumulate, uint64_t b_bytes, hipStream_t st) {
+                    int32_t accumulate, uint64_t b_bytes, float* partials, hipStream_t st) {
     if (b_bytes + 64u * 4u * (uint64_t)VEC >= kBufferLimit)
-        return launch_one<VEC, 64, R, false>(d, B, O, ld, C, accumulate, 0u, st);
+        return launch_one<VEC, 64, R, false>(d, B, O, ld, C, accumulate, 0u, partials, st);
     const uint32_t bb = (uint32_t)b_bytes;
     // Lanes per entry: the smallest power of two covering O, at least 8 (at
     // most 8 streams per wave, so every stream gets several tiles); 8 lanes
     // occur for VEC = 4 (O = 32) and VEC = 1 (O <= 8).
     const int32_t need = (O + VEC - 1) / VEC;
     if constexpr (VEC == 1 || VEC == 4) {
-        if (need <= 8) return launch_one<VEC, 8, R, true>(d, B, O, ld, C, accumulate, bb, st);
+        if (need <= 8)
+            return launch_one<VEC, 8, R, true>(d, B, O, ld, C, accumulate, bb, partials, st);
     }
-    if (need <= 16) return launch_one<VEC, 16, R, true>(d, B, O, ld, C, accumulate, bb, st);
-    if (need <= 32) return launch_one<VEC, 32, R, true>(d, B, O, ld, C, accumulate, bb, st);
-    return launch_one<VEC, 64, R, true>(d, B, O, ld, C, accumulate, bb, st);
+    if (need <= 16) return launch_one<VEC, 16, R, true>(d, B, O, ld, C, accumulate, bb, partials, st);
+    if (need <= 32) return launch_one<VEC, 32, R, true>(d, B, O, ld, C, accumulate, bb, partials, st);
+    return launch_one<VEC, 64, R, true>(d, B, O, ld, C, accumulate, bb, partials, st);
 }
 
 // Columns [0, O) of B and C, whose rows are ld floats apart (B and C point
 // at the first column; ld > O for one column slice of wider matrices).
 template <int VEC>
 hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, int32_t ld,
-                      float* C, int32_t accumulate, hipStream_t st) {
+                      float* C, int32_t accumulate, float* partials, hipStream_t st) {
     if (d.tv_n_chunks > 0) {
         // Bytes from B to the end of its last row.
         const uint64_t b_bytes = v.N > 0 ? ((uint64_t)(v.N - 1) * (uint64_t)ld + (uint64_t)O) * 4u : 0u;
         hipError_t e;
         switch (d.tv_R) {
-            case 1: e = launch_r<VEC, 1>(d, B, O, ld, C, accumulate, b_bytes, st); break;
-            case 2: e = launch_r<VEC, 2>(d, B, O, ld, C, accumulate, b_bytes, st); break;
-            case 3: e = launch_r<VEC, 3>(d, B, O, ld, C, accumulate, b_bytes, st); break;
-            case 4: e = launch_r<VEC, 4>(d, B, O, ld, C, accumulate, b_bytes, st); break;
-            case 8: e = launch_r<VEC, 8>(d, B, O, ld, C, accumulate, b_bytes, st); break;
+            case 1: e = launch_r<VEC, 1>(d, B, O, ld, C, accumulate, b_bytes, partials, st); break;
+            case 2: e = launch_r<VEC, 2>(d, B, O, ld, C, accumulate, b_bytes, partials, st); break;
+            case 3: e = launch_r<VEC, 3>(d, B, O, ld, C, accumulate, b_bytes, partials, st); break;
+            case 4: e = launch_r<VEC, 4>(d, B, O, ld, C, accumulate, b_bytes, partials, st); break;
+            case 8: e = launch_r<VEC, 8>(d, B, O, ld, C, accumulate, b_bytes, partials, st); break;
             case kTileMmaRows:
                 // 16-row tiles are never column-sliced: their rows are O apart.
                 if (ld != O) return hipErrorInvalidValue;
-                e = launch_mma<VEC>(v, d, B, O, C, accumulate, st);
+                e = launch_mma<VEC>(v, d, B, O, C, accumulate, partials, st);
                 break;
             default: return hipErrorInvalidValue;
         }
@@ -760,7 +762,7 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
     }
     if (d.tv_n_split > 0) {
         hipLaunchKernelGGL(vcsr_tile_reduce<VEC>, dim3((unsigned)d.tv_n_split), dim3(256), 0, st,
-                           O, ld, accumulate, reinterpret_cast<const int4*>(d.tv_split), d.partials,
+                           O, ld, accumulate, reinterpret_cast<const int4*>(d.tv_split), partials,
                            C);
         return hipGetLastError();
     }
@@ -779,34 +781,50 @@ static int tile_vec(int32_t O, bool a16, bool a8, bool mma) {
     return 1;
 }
 
-hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
-                            float* C, int32_t accumulate, hipStream_t st) {
-    if (O <= 0 || v.M == 0) return hipSuccess;
+// Floats per lane (tile_vec) and column-slice width of a launch over B and
+// C of width O.  Tiles of 1 to 8 rows with 16-byte vectors: one launch per
+// column slice of at most 256 columns (one column tile of a wave), or 128
+// when B is over 512 MB, so that the B bytes live at a time stay small.
+// Measured against one launch over all columns: banded 62K matrix, slices of
+// 256, O = 512 / 1024 / 2048: same / 16% / 30% faster; slices of 128,
+// uniform-random 1M matrix O = 256 (1 GB): 11% faster, power-law 322K
+// matrix O = 512 (659 MB): 3% faster, O = 256 (330 MB): 3% slower.
+struct TileSlicing {
+    int vec;
+    int32_t width;
+};
+static TileSlicing tile_slicing(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                                const float* C) {
     const bool a16 = (((uintptr_t)B | (uintptr_t)C) & 15u) == 0;
     const bool a8 = (((uintptr_t)B | (uintptr_t)C) & 7u) == 0;
     // Narrow B: narrower per-lane vectors give streams of at least 8-16
     // lanes, so fewer streams share a tile's entries (measured at O = 8:
     // 4-byte loads with 8 streams 1.3x faster than 16-byte loads with 32).
-    const int vec = tile_vec(O, a16, a8, d.tv_R == kTileMmaRows);
-    // Tiles of 1 to 8 rows with 16-byte vectors: one launch per column slice
-    // of at most 256 columns (one column tile of a wave), or 128 when B is
-    // over 512 MB, so that the B bytes live at a time stay small.  Measured
-    // against one launch over all columns: banded 62K matrix, slices of 256,
-    // O = 512 / 1024 / 2048: same / 16% / 30% faster; slices of 128,
-    // uniform-random 1M matrix O = 256 (1 GB): 11% faster, power-law 322K
-    // matrix O = 512 (659 MB): 3% faster, O = 256 (330 MB): 3% slower.
-    int32_t W = O;
-    if (vec == 4 && d.tv_R != kTileMmaRows) {
-        if ((uint64_t)v.N * (uint64_t)O * 4u > kTileSliceBytes) W = std::min(O, kTileSliceCols);
-        else W = std::min(O, kTileWideCols);
+    TileSlicing ts{tile_vec(O, a16, a8, d.tv_R == kTileMmaRows), O};
+    if (ts.vec == 4 && d.tv_R != kTileMmaRows) {
+        if ((uint64_t)v.N * (uint64_t)O * 4u > kTileSliceBytes) ts.width = std::min(O, kTileSliceCols);
+        else ts.width = std::min(O, kTileWideCols);
     }
-    for (int32_t c0 = 0; c0 < O; c0 += W) {
-        const int32_t w = std::min(W, O - c0);
+    return ts;
+}
+
+int64_t tile_partials_floats(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                             const float* C) {
+    if (O <= 0 || v.M == 0 || d.tv_partial_rows == 0) return 0;
+    return (int64_t)d.tv_partial_rows * tile_slicing(v, d, B, O, C).width;
+}
+
+hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                            float* C, int32_t accumulate, float* partials, hipStream_t st) {
+    if (O <= 0 || v.M == 0) return hipSuccess;
+    const TileSlicing ts = tile_slicing(v, d, B, O, C);
+    for (int32_t c0 = 0; c0 < O; c0 += ts.width) {
+        const int32_t w = std::min(ts.width, O - c0);
         hipError_t e;
-        switch (vec) {
-            case 4: e = launch_vec<4>(v, d, B + c0, w, O, C + c0, accumulate, st); break;
-            case 2: e = launch_vec<2>(v, d, B + c0, w, O, C + c0, accumulate, st); break;
-            default: e = launch_vec<1>(v, d, B + c0, w, O, C + c0, accumulate, st); break;
+        switch (ts.vec) {
+            case 4: e = launch_vec<4>(v, d, B + c0, w, O, C + c0, accumulate, partials, st); break;
+            case 2: e = launch_vec<2>(v, d, B + c0, w, O, C + c0, accumulate, partials, st); break;
+            default: e = launch_vec<1>(v, d, B + c0, w, O, C + c0, accumulate, partials, st); break;
         }
         if (e != hipSuccess) return e;
     }
