@@ -212,9 +212,11 @@ enum {
     VCSR_KERNEL_ROW = 3,     /* row-stationary: one wavefront per C row walks the
                                 row's (group, lane) slots; C written once, no
                                 atomics                                         */
-    VCSR_KERNEL_TILE = 4     /* tile-stationary: runs of up to 8 consecutive rows
-                                sharing columns are walked together, each B row
-                                slice loaded once per tile; C written once     */
+    VCSR_KERNEL_TILE = 4     /* tile-stationary: runs of 1, 2, 3, 4 or 8
+                                consecutive rows sharing columns are walked
+                                together on the vector ALUs, and 16-row tiles
+                                (dense sub-blocks) on FP32 MFMA; each B row
+                                slice loaded once per tile; C written once    */
 };
 
 /* spmm_vcsr with an explicit kernel and C semantics: accumulate = 1 gives

@@ -73,6 +73,17 @@ def row_abs_sums(row_ptr, val):
     return np.bincount(rows, weights=np.abs(np.asarray(val, dtype=np.float64)), minlength=M)
 
 
+def host_threads():
+    """Threads for the oracle's whole-matrix products: the cores this
+    process may use, at most 16 (one GPU's share of the GPU box's host) and
+    at most OMP_NUM_THREADS when that is set."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, min(n, 16))
+
+
 def assert_within_tolerance(C, ref64, row_ptr, val, B, what=""):
     row_l1 = row_abs_sums(row_ptr, val)
     bmax = float(np.abs(B).max()) if B.size else 0.0

@@ -12,8 +12,11 @@ Contents (all data, no code):
   * csr:   COO inputs (with duplicate and unsorted columns) and the CSR that
            the reference's coo_to_csr returns;
   * tiny:  small CSR matrices and the full VCSR arrays of layouts H, S and TC;
-  * large: for synthetic configs cfg1 (seed 0), cfg2 and cfg5, a SHA-256 of
-           the CSR input (to pin the generator) and of every VCSR array.
+  * large: for synthetic configs cfg1 (seed 0), cfg2, cfg3, cfg4 and cfg5,
+           a SHA-256 of the CSR input (to pin the generator) and of every
+           VCSR array.  cfg3 and cfg4 have layout S only (segw 4; cfg4 also
+           segw 8): the reference's layout-H builder allocates S*M entry
+           lists (include/vcsr.hpp:33), 26e9 for cfg3.
 
 Run from the repository root after __graft_entry__.build():
     python tests/golden/make_golden.py
@@ -152,7 +155,8 @@ def main():
         out["tiny"][name] = entry
 
     for cfg, fmts in [(1, [(0, 4, 64), (1, 4, 64), (0, 4, 32), (1, 4, 32), (2, 16, 16)]),
-                      (2, [(1, 4, 64), (1, 4, 32)]), (5, [(2, 16, 16)])]:
+                      (2, [(1, 4, 64), (1, 4, 32)]), (3, [(1, 4, 64)]),
+                      (4, [(1, 4, 64), (1, 8, 64)]), (5, [(2, 16, 16)])]:
         csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
         rp, col, val = orc.ref_coo_to_csr(csr.M, csr.N, *[
             np.asarray(x) for x in (vs.generate_coo(cfg, 0).rows, vs.generate_coo(cfg, 0).cols,

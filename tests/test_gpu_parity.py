@@ -6,15 +6,17 @@ oracle (oracle/vcsr_oracle.cpp) on the same seeded inputs.
     atomics -> north-star tolerance (rel L2 <= 1e-5, per-row max-abs <=
     1e-4 * ||A_r||_1 * max|B|) against the oracle's double-accumulated sum,
     and the same against its FP32 sum;
-  * full-size configs: per-row oracle check on sampled rows plus the
-    size-independent column-sum identity sum_r C[r,:] = (1^T A) B.
+  * full-size configs (every BASELINE config point on the default path):
+    every element of C against the oracle's double sum under the same
+    bounds, plus the size-independent column-sum identity
+    sum_r C[r,:] = (1^T A) B.
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from conftest import assert_within_tolerance, random_csr, row_abs_sums
+from conftest import assert_within_tolerance, host_threads, random_csr, row_abs_sums
 
 pytestmark = pytest.mark.gpu
 
@@ -163,22 +165,13 @@ def test_vcsr_repeat_runs_agree(gpu, orc, st):
 
 
 # ------------------------------------------------- full-size configurations
-def _rowsample_check(vs, orc, csr, B, C, nrows, seed):
-    rng = np.random.default_rng(seed)
-    rows = np.unique(np.concatenate([rng.choice(csr.M, size=min(nrows, csr.M), replace=False),
-                                     [0, csr.M - 1], [int(np.argmax(np.diff(csr.row_ptr)))]]))
-    rp = np.zeros(len(rows) + 1, np.int64)
-    cols, vals = [], []
-    for i, r in enumerate(rows):
-        s, e = csr.row_ptr[r], csr.row_ptr[r + 1]
-        cols.append(csr.col[s:e])
-        vals.append(csr.val[s:e])
-        rp[i + 1] = rp[i] + (e - s)
-    cols = np.concatenate(cols).astype(np.int32)
-    vals = np.concatenate(vals).astype(np.float32)
-    rp = rp.astype(np.int32)
-    ref64 = orc.spmm_f64(len(rows), rp, cols, vals, B)
-    assert_within_tolerance(C[rows], ref64, rp, vals, B, "sampled rows")
+def _whole_check(orc, csr, B, C, what):
+    """Every element of C against the oracle's double-accumulated product
+    (rows split over the host's threads; the same sum as one thread)."""
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B, host_threads())
+    rel, worst = assert_within_tolerance(C, ref64, csr.row_ptr, csr.val, B, what)
+    print(f"{what}: rel L2 {rel:.2e}, max-abs / bound {worst:.4f}", flush=True)
+    return ref64
 
 
 def _colsum_check(csr, B, C):
@@ -199,8 +192,34 @@ def test_full_size_configs(gpu, orc, st, cfg, O, segw, tileK, layout, kind):
     B = vs.gen_dense(cfg, 1 if cfg == 5 else 0, csr.N, O)
     bundle = 16 if layout == 2 else 64
     C = _run(vs, kind, csr, B, st, layout=layout, segw=segw, bundle=bundle, tileK=tileK)
-    _rowsample_check(vs, orc, csr, B, C, 2000, cfg)
+    _whole_check(orc, csr, B, C, f"cfg{cfg} O={O} {kind}")
     _colsum_check(csr, B, C)
+
+
+# (cfg, O, segw, layout): every O of the BASELINE configs, cfg4 at both segw.
+BASELINE_POINTS = [(2, 8, 4, 1), (2, 32, 4, 1), (2, 128, 4, 1), (2, 512, 4, 1), (3, 8, 4, 1),
+                   (3, 128, 4, 1), (4, 256, 4, 1), (4, 256, 8, 1), (5, 512, 16, 2)]
+
+
+@pytest.mark.parametrize("cfg,O,segw,layout", BASELINE_POINTS)
+def test_baseline_config_points_whole_c(gpu, orc, st, cfg, O, segw, layout):
+    """The default path (spmm_vcsr: VCSR_KERNEL_AUTO, the reference's C +=
+    A*B on a zeroed C) at every BASELINE config point and full size: all of
+    C within the north-star bounds of the oracle's double sum.  cfg5's
+    16-row tiles are never split (816 entries each), so its C is also the
+    oracle's FP32 loop bit for bit."""
+    vs = gpu
+    print(f"baseline point cfg{cfg} O={O} segw={segw} layout={layout}", flush=True)
+    csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
+    B = vs.gen_dense(cfg, 1 if cfg == 5 else 0, csr.N, O)
+    bundle = 16 if layout == 2 else 64
+    C = _run(vs, "vcsr", csr, B, st, layout=layout, segw=segw, bundle=bundle,
+             tileK=64 if cfg == 2 else 128)
+    _whole_check(orc, csr, B, C, f"cfg{cfg} O={O} segw={segw}")
+    _colsum_check(csr, B, C)
+    if cfg == 5:
+        ref32 = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B, host_threads())
+        assert np.array_equal(C.view(np.uint32), ref32.view(np.uint32))
 
 
 def test_full_size_csr_naive_cfg2(gpu, orc, st):
@@ -276,7 +295,7 @@ def test_full_size_row_kernel(gpu, orc, st, cfg, O, layout, kind):
     B = vs.gen_dense(cfg, 1 if cfg == 5 else 0, csr.N, O)
     segw, bundle = (16, 16) if layout == 2 else (4, 64)
     C = _run(vs, kind, csr, B, st, layout=layout, segw=segw, bundle=bundle, tileK=128)
-    _rowsample_check(vs, orc, csr, B, C, 1500, cfg)
+    _whole_check(orc, csr, B, C, f"cfg{cfg} O={O} {kind}")
     _colsum_check(csr, B, C)
 
 
@@ -343,9 +362,14 @@ def test_tile_kernel_split_tiles(gpu, orc, st, tile_rows):
         assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B, f"R{tile_rows} O{O}")
 
 
-@pytest.mark.parametrize("kind,tile_rows", [("csr", 4), ("segment", 4), ("row", 4), ("tile", 4),
-                                            ("tile", 16)])
-def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind, tile_rows):
+@pytest.mark.parametrize("kind,tile_rows,O", [
+    ("csr", 4, 36), ("segment", 4, 36), ("row", 4, 36), ("tile", 4, 36), ("tile", 16, 36),
+    # 1- and 3-row tiles (B row inside the value record), 8-row tiles, and
+    # narrow B: single-row tiles merge four work items per wave at O <= 8
+    # and O = 32, and redo non-finite pieces across the merged items.
+    ("tile", 1, 36), ("tile", 3, 36), ("tile", 8, 36), ("tile", 1, 8), ("tile", 3, 8),
+    ("tile", 1, 32), ("tile", 2, 8), ("row", 4, 8)])
+def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind, tile_rows, O):
     """Inf and NaN in B reach exactly the C entries whose rows have a nonzero
     in that B row (an absent entry contributes nothing, not 0 * inf).  The
     MFMA kernel is left out: it multiplies every group as a dense tile, so a
@@ -354,7 +378,6 @@ def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind, tile_rows):
     vs = gpu
     rng = np.random.default_rng(11)
     csr = _block_csr(vs, rng, 20, 4, 120, 5, 3, 0.6)
-    O = 36
     B = vs.gen_dense(4, 0, csr.N, O)
     B[5, 3] = np.inf
     B[17, :] = np.nan
@@ -386,7 +409,7 @@ def test_b_of_2gb_or_more_uses_64bit_addresses(gpu, orc, st, kind, tile_rows):
     B = vs.gen_dense(77, 0, N, O)
     assert B.nbytes >= 1 << 31
     C = _run(vs, kind, csr, B, st, layout=1, segw=4, bundle=64, tileK=128, tile_rows=tile_rows)
-    _rowsample_check(vs, orc, csr, B, C, 300, 21)
+    _whole_check(orc, csr, B, C, f"2 GiB B {kind} R={tile_rows}")
 
 
 @pytest.mark.parametrize("accumulate", [False, True])
