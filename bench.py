@@ -14,6 +14,9 @@ reset inside the step.  --cols replaces a config's O (column sweeps).  K steps a
 warm-up steps; `value` is 2*nnz*O*K / that time.  `kernel_ms` is the kernel
 alone, K back-to-back launches between events on its stream (the reference
 times kernels only, src/kernels.cu:153-162); the roofline uses it.
+`ms_per_step_median` is the median per-step time of a second pass of K
+steps timed in 10 groups of K/10.  The default kernel's launch shape (tile
+height, column slices, reduce launches) is named in `config`.
 
 Prints ONE JSON line.  Multi-GPU runs are not part of this build.
 """
@@ -274,15 +277,21 @@ def main():
     lib.vcsr_device_sync()
     C = dC.numpy(st)
 
-    # Per-step durations for the median: a second pass of K steps with an
-    # event between consecutive steps (the headline uses the first pass).
-    evs = [vs.Event() for _ in range(args.steps + 1)]
+    # Per-step durations for the median: a second pass of K steps in (up to)
+    # 10 groups of g consecutive steps with an event between groups, so that
+    # an event record (a few us on this device) is spread over g steps; the
+    # median is taken over the groups' per-step times (the headline uses
+    # the first pass).
+    g = max(1, args.steps // 10)
+    ngroups = args.steps // g
+    evs = [vs.Event() for _ in range(ngroups + 1)]
     lib.vcsr_device_sync()
     evs[0].record(st)
-    for i in range(args.steps):
-        step()
+    for i in range(ngroups):
+        for _ in range(g):
+            step()
         evs[i + 1].record(st)
-    step_ms = [evs[i].elapsed_ms(evs[i + 1]) for i in range(args.steps)]
+    step_ms = [evs[i].elapsed_ms(evs[i + 1]) / g for i in range(ngroups)]
     lib.vcsr_device_sync()
 
     # Correctness of the last step of the first pass: every element of C
@@ -308,6 +317,25 @@ def main():
     else:
         kernel_ms = total_ms / args.steps
 
+    config = {"workload": f"{args.config}: {csr.M}x{csr.N} nnz={csr.nnz} O={O}",
+              "algo": args.algo, "segw": segw, "bundle": bundle,
+              "layout": ["H", "S", "TC"][layout] if fmt is not None else "csr",
+              "step": "C reset + SpMM kernel (C += A*B)" if needs_reset
+              else "SpMM kernel writing C = A*B"}
+    if fmt is not None and kern in (vs.KERNEL_AUTO, vs.KERNEL_TILE):
+        # The tile-stationary kernel walks the row-tile view (derived from the
+        # VCSR slots at upload); segw/bundle shape the format it comes from,
+        # tileK is the column tile of the segment-major kernels only.
+        li = fmt.launch_info(O, kern)
+        config.update({
+            "timed_kernel": ("vcsr_tile_mma_kernel (16-row tiles on FP32 MFMA)"
+                             if li["matrix_cores"] else "vcsr_tile_kernel (row-tile view)"),
+            "tile_rows": li["tile_rows"], "tiles": li["tiles"], "entries": li["entries"],
+            "column_slices": li["column_slices"], "slice_cols": li["slice_cols"],
+            "reduce_launches": li["reduce_launches"],
+            "tileK": f"{tileK} (not used by the timed kernel)"})
+    elif fmt is not None:
+        config["tileK"] = tileK
     flop = 2.0 * csr.nnz * O
     ms_per_step = total_ms / args.steps
     value = flop / (ms_per_step * 1e-3) / 1e9
@@ -327,12 +355,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"{args.config}: {csr.M}x{csr.N} nnz={csr.nnz} O={O}",
-                   "algo": args.algo, "segw": segw, "bundle": bundle, "tileK": tileK,
-                   "layout": ["H", "S", "TC"][layout] if args.algo not in ("csr", "aspt", "rocsparse")
-                   else "csr",
-                   "step": "C reset + SpMM kernel (C += A*B)" if needs_reset
-                   else "SpMM kernel writing C = A*B"},
+        "config": config,
         "kernel_ms": round(kernel_ms, 5),
         "kernel_gflops": round(flop / (kernel_ms * 1e-3) / 1e9, 2),
         "check": {"rows": "all", "rel_l2": rel, "maxabs_over_bound": round(worst, 4),

@@ -269,6 +269,29 @@ int vcsr_mfma_work(const vcsr_fmt* fmt, int32_t O, int32_t tileK, int64_t* ops,
  * No reference counterpart. */
 int vcsr_tile_mfma_work(const vcsr_fmt* fmt, int32_t O, int64_t* ops, int32_t* flops_per_op);
 
+/* What one SpMM of width O with `kernel` (VCSR_KERNEL_AUTO resolved) launches
+ * on an uploaded format, for reports that name the timed work.  For the
+ * tile-stationary kernel: the row-tile view (tile height, tiles, entries =
+ * B-row slice loads per column tile), whether its tiles run on the FP32
+ * matrix cores, floats per lane, column slices (one launch each) and their
+ * width, reduce-kernel launches and split rows, and the partial-row floats
+ * of scratch; other kernels report only `kernel`.  As launched on 16-byte
+ * aligned B and C.  No reference counterpart. */
+typedef struct {
+    int32_t kernel;
+    int32_t tile_rows;
+    int64_t tiles;
+    int64_t entries;
+    int32_t matrix_cores;
+    int32_t vec;
+    int32_t column_slices;
+    int32_t slice_cols;
+    int32_t reduce_launches;
+    int32_t split_rows;
+    int64_t scratch_floats;
+} vcsr_launch_info;
+int vcsr_launch_info_get(const vcsr_fmt* fmt, int32_t O, int32_t kernel, vcsr_launch_info* out);
+
 /* ------------------------------------------------------ vendor baseline */
 /* rocSPARSE SpMM (CSR int32 x row-major dense, FP32, default algorithm,
  * C = A*B) on caller-owned device arrays: the counterpart of

@@ -58,6 +58,9 @@ def test_gpu_entry_points_without_gpu(vs):
     lib = vs.load_library()
     rc = lib.spmm_vcsr(fmt._h, None, 8, 64, None, None, None)
     assert rc == vs.VCSR_ESTATE  # not uploaded: refused before any device work
+    with pytest.raises(vs.VcsrError) as e:
+        fmt.launch_info(64)
+    assert e.value.code == vs.VCSR_ESTATE
     rc = lib.spmm_csr_naive(4, None, None, None, None, 8, None, None, None)
     assert rc == vs.VCSR_EINVAL
 

@@ -769,3 +769,40 @@ def test_tile_kernel_property(gpu, orc, st, M, N, bh, keep, tile_rows, fixed, O,
     n = int(np.diff(csr.row_ptr).max())
     bound = max(1e-5 * np.linalg.norm(ref64), n * 2.0 ** -24 * np.linalg.norm(absref))
     assert np.linalg.norm(got - ref64) <= bound + np.linalg.norm(slack), f"{what}: rel L2"
+
+
+def test_launch_info_names_what_runs(gpu, orc, st):
+    """vcsr_launch_info_get reports the default kernel's launch shape: the
+    row-tile view, column slices of 256 columns (128 once B exceeds 512 MB),
+    the matrix-core path for 16-row tiles, and reduce launches and scratch
+    only when tiles are split."""
+    vs = gpu
+    csr = vs.coo_to_csr(vs.generate_coo(1, 0))
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.upload(st)
+    r, tiles, entries = fmt.tile_info()
+    li = fmt.launch_info(512)
+    assert li["kernel"] == vs.KERNEL_TILE and li["tile_rows"] == r
+    assert (li["tiles"], li["entries"]) == (tiles, entries)
+    assert (li["column_slices"], li["slice_cols"], li["vec"]) == (2, 256, 4)
+    assert li["matrix_cores"] == 0 and li["reduce_launches"] == 0 and li["scratch_floats"] == 0
+    assert fmt.launch_info(8)["column_slices"] == 1
+    assert fmt.launch_info(64, vs.KERNEL_SEGMENT)["kernel"] == vs.KERNEL_SEGMENT
+    # Long rows: split tiles, one reduce launch per slice, partial rows x slice width.
+    rng = np.random.default_rng(2)
+    lens = np.where(np.arange(200) % 10 == 0, 900, 8)
+    rows = np.repeat(np.arange(200, dtype=np.int32), lens)
+    cols = np.concatenate([rng.choice(5000, size=n, replace=False) for n in lens]).astype(np.int32)
+    long = vs.coo_to_csr(vs.Coo.from_arrays(200, 5000, rows, cols,
+                                            rng.uniform(-1, 1, rows.size).astype(np.float32)))
+    f2 = vs.build_vcsr(long, 4, 64, vs.LAYOUT_S)
+    f2.upload(st)
+    li2 = f2.launch_info(300)
+    assert li2["column_slices"] == 2 and li2["reduce_launches"] == 2 and li2["split_rows"] == 20
+    assert li2["scratch_floats"] > 0 and li2["scratch_floats"] % 256 == 0
+    # 16-row dense blocks run on the matrix cores, never column-sliced.
+    blk = _block_csr(vs, rng, 8, 16, 256, 4, 16, 1.0)
+    f3 = vs.build_vcsr(blk, 16, 16, vs.LAYOUT_TC)
+    f3.upload(st)
+    li3 = f3.launch_info(512)
+    assert li3["tile_rows"] == 16 and li3["matrix_cores"] == 1 and li3["column_slices"] == 1

@@ -43,7 +43,7 @@ EXPORTS = (
     "vcsr_csr_view_get vcsr_csr_free vcsr_build vcsr_fmt_arrays vcsr_fmt_save vcsr_fmt_load "
     "vcsr_fmt_upload "
     "vcsr_fmt_set_tile_rows vcsr_fmt_set_tile_windows vcsr_fmt_tile_info vcsr_fmt_free spmm_csr_naive spmm_csr_wave spmm_vcsr "
-    "spmm_vcsr_ex spmm_vcsr_noalloc spmm_vcsr_mfma vcsr_mfma_work vcsr_tile_mfma_work spmm_csr_cpu "
+    "spmm_vcsr_ex spmm_vcsr_noalloc spmm_vcsr_mfma vcsr_mfma_work vcsr_launch_info_get vcsr_tile_mfma_work spmm_csr_cpu "
     "vcsr_vendor_plan_create vcsr_vendor_spmm vcsr_vendor_plan_free spmm_csr_vendor "
     "vcsr_device_count vcsr_device_name vcsr_dev_malloc vcsr_dev_free vcsr_memcpy_h2d "
     "vcsr_memcpy_d2h vcsr_memcpy_d2d vcsr_memset_d vcsr_stream_create vcsr_stream_destroy "
@@ -68,6 +68,14 @@ class _CsrView(C.Structure):
     _fields_ = [("M", C.c_int32), ("N", C.c_int32), ("nnz", C.c_int32),
                 ("row_ptr", C.POINTER(C.c_int32)), ("col", C.POINTER(C.c_int32)),
                 ("val", C.POINTER(C.c_float))]
+
+
+class _LaunchInfo(C.Structure):
+    _fields_ = [("kernel", C.c_int32), ("tile_rows", C.c_int32), ("tiles", C.c_int64),
+                ("entries", C.c_int64), ("matrix_cores", C.c_int32), ("vec", C.c_int32),
+                ("column_slices", C.c_int32), ("slice_cols", C.c_int32),
+                ("reduce_launches", C.c_int32), ("split_rows", C.c_int32),
+                ("scratch_floats", C.c_int64)]
 
 
 class _Arrays(C.Structure):
@@ -122,6 +130,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "spmm_vcsr_noalloc": (C.c_int, [P, P, I32, P, P, I32]),
         "spmm_vcsr_mfma": (C.c_int, [P, P, I32, P, P, pF]),
         "vcsr_mfma_work": (C.c_int, [P, I32, I32, C.POINTER(I64), pI]),
+        "vcsr_launch_info_get": (C.c_int, [P, I32, I32, C.POINTER(_LaunchInfo)]),
         "vcsr_tile_mfma_work": (C.c_int, [P, I32, C.POINTER(I64), pI]),
         "spmm_csr_cpu": (C.c_int, [I32, P, P, P, P, I32, P, I32]),
         "vcsr_vendor_plan_create": (C.c_int, [I32, I32, I32, P, P, P, P, I32, P, P,
@@ -298,6 +307,13 @@ class Vcsr:
         """Fixed row windows of the tile height instead of shared-column
         tiles (16 rows: FastSpMM's condensed tiles); before upload()."""
         _check(load_library().vcsr_fmt_set_tile_windows(self._h, 1 if fixed else 0))
+
+    def launch_info(self, O: int, kernel: int = 0) -> dict:
+        """What one SpMM of width O launches (vcsr_launch_info_get): kernel,
+        row-tile view, column slices, reduce launches, scratch floats."""
+        info = _LaunchInfo()
+        _check(load_library().vcsr_launch_info_get(self._h, O, kernel, C.byref(info)))
+        return {name: getattr(info, name) for name, _ in _LaunchInfo._fields_}
 
     def tile_info(self) -> tuple[int, int, int]:
         """(tile height, tiles, entries) of the uploaded row-tile view."""

@@ -55,6 +55,18 @@ hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, i
                             float* C, int32_t accumulate, float* partials, hipStream_t st);
 int64_t tile_partials_floats(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                              const float* C);
+// What launch_vcsr_tile launches for these B and C: floats per lane, column
+// slices (one launch each), whether the tiles run on the matrix cores, the
+// reduce launches and the partial-row floats.
+struct TilePlan {
+    int vec = 0;
+    int32_t slice_cols = 0, slices = 0;
+    bool matrix_cores = false;
+    int32_t reduce_launches = 0;
+    int64_t partial_floats = 0;
+};
+TilePlan tile_launch_plan(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                          const float* C);
 // MFMA instructions launch_vcsr_tile issues for one SpMM of width O when
 // the view has 16-row tiles (none otherwise), as launched for the alignment
 // of 16-byte aligned B and C.

@@ -365,6 +365,32 @@ int spmm_vcsr_mfma(const vcsr_fmt* fmt, const float* dB, int32_t O, float* dC, v
     return spmm_vcsr_ex(fmt, dB, O, 0, dC, stream, ms, VCSR_KERNEL_MFMA, 1);
 }
 
+int vcsr_launch_info_get(const vcsr_fmt* fmt, int32_t O, int32_t kernel, vcsr_launch_info* out) {
+    return guarded([&] {
+        need(fmt && out, "null argument");
+        need(O >= 0, "negative O");
+        need(kernel >= VCSR_KERNEL_AUTO && kernel <= VCSR_KERNEL_TILE, "unknown kernel");
+        if (!fmt->dev.uploaded) throw vcsr::Error(VCSR_ESTATE, "format not uploaded");
+        std::memset(out, 0, sizeof *out);
+        out->kernel = kernel == VCSR_KERNEL_AUTO ? VCSR_KERNEL_TILE : kernel;
+        if (out->kernel != VCSR_KERNEL_TILE) return;
+        const DeviceFmt& d = fmt->dev;
+        // As launched on 16-byte aligned B and C (device allocations are).
+        const float* aligned = reinterpret_cast<const float*>(uintptr_t(256));
+        const vcsr::TilePlan p = vcsr::tile_launch_plan(fmt->v, d, aligned, O, aligned);
+        out->tile_rows = d.tv_R;
+        out->tiles = fmt->tv_tiles;
+        out->entries = d.tv_n_entries;
+        out->matrix_cores = p.matrix_cores ? 1 : 0;
+        out->vec = p.vec;
+        out->column_slices = p.slices;
+        out->slice_cols = p.slice_cols;
+        out->reduce_launches = p.reduce_launches;
+        out->split_rows = d.tv_n_split;
+        out->scratch_floats = p.partial_floats;
+    });
+}
+
 int vcsr_mfma_work(const vcsr_fmt* fmt, int32_t O, int32_t tileK, int64_t* ops,
                    int32_t* flops_per_op) {
     return guarded([&] {

@@ -814,6 +814,20 @@ int64_t tile_partials_floats(const Vcsr& v, const DeviceFmt& d, const float* B, 
     return (int64_t)d.tv_partial_rows * tile_slicing(v, d, B, O, C).width;
 }
 
+TilePlan tile_launch_plan(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
+                          const float* C) {
+    TilePlan p;
+    if (O <= 0 || v.M == 0) return p;
+    const TileSlicing ts = tile_slicing(v, d, B, O, C);
+    p.vec = ts.vec;
+    p.slice_cols = ts.width;
+    p.slices = (O + ts.width - 1) / ts.width;
+    p.matrix_cores = d.tv_R == kTileMmaRows && d.tv_n_chunks > 0;
+    p.reduce_launches = d.tv_n_split > 0 ? p.slices : 0;
+    p.partial_floats = tile_partials_floats(v, d, B, O, C);
+    return p;
+}
+
 hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                             float* C, int32_t accumulate, float* partials, hipStream_t st) {
     if (O <= 0 || v.M == 0) return hipSuccess;
