@@ -122,54 +122,63 @@ __device__ __forceinline__ float fma_zero_acc(float4 x, float z) {
                           __builtin_fmaf(x.x, 0.f, z))));
 }
 
-// One wave per MERGE consecutive work items of the view.  BUF: B smaller than
-// 2 GB, read with raw buffer loads at 32-bit byte offsets; otherwise 64-bit
-// addresses from B row indices (LPE = 64 only).  Up to 3 tile rows (one work
-// item per wave) the register budget is held to 5 waves per SIMD: measured
-// faster than 4 on the banded workload; 6 spills, and so does 5 with 4 rows.
-template <int VEC, int LPE, int R, int MERGE, bool BUF>
-__global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu((R <= 3 && MERGE == 1) ? 5 : 1, 8)))
-void vcsr_tile_kernel(
-    int32_t n_chunks, int32_t O, int32_t ld, int32_t accumulate, uint32_t b_bytes,
-    const int4* __restrict__ chunks, const int4* __restrict__ pieces,
-    const int32_t* __restrict__ ent_brow, const uint16_t* __restrict__ ent_mask,
-    const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
-    float* __restrict__ partials) {
-    using V = typename VecT<VEC>::T;
-    constexpr int S = 64 / LPE;                              // streams per wave
-    constexpr int RS = tile_slot_stride(R);                  // slots stored per entry
-    constexpr bool FOLD = tile_dev_folds_brow(R);            // B row inside the values
-    constexpr int DS = tile_dev_stride(R);                   // floats per entry in ent_val
-    constexpr int EMAX = tile_piece_entries(R) * MERGE;      // entries per wave
-    constexpr int PMAX = kTileChunkPieces * MERGE;           // pieces per wave
+// Compile-time shape of the per-wave LDS of the VALU tile kernel.
+template <int VEC, int LPE, int R, int MERGE>
+struct TileShape {
+    static constexpr int S = 64 / LPE;                          // streams per wave
+    static constexpr int RS = tile_slot_stride(R);              // slots stored per entry
+    static constexpr int EMAX = tile_piece_entries(R) * MERGE;  // entries per wave
+    static constexpr int PMAX = kTileChunkPieces * MERGE;       // pieces per wave
     // Loads per block: 8, or 4 when 8+ streams split a tall tile's entries
     // (fewer padded entries per block: banded 62K matrix, O = 8 / 32, 3%
     // faster; single-row tiles, which merge four items, measured slower).
-    constexpr int U = (S >= 8 && R > 1) ? 4 : 8;
+    static constexpr int U = (S >= 8 && R > 1) ? 4 : 8;
     // A one-piece item's list is padded with "no row" entries of value 0 up
     // to a multiple of S*UT, so that its blocks are full blocks of U loads
     // per stream and at most one each of U/2, U/4, ... UT (UT = 2).
-    constexpr int UT = U >= 2 ? 2 : U;
-    constexpr int EPAD = (EMAX + S * U - 1) / (S * U) * (S * U);
-    __shared__ uint32_t s_brow[kWaves][EPAD];
-    __shared__ uint8_t s_bad[kWaves][PMAX];
-    __shared__ __align__(16) float s_val[kWaves][EPAD * RS];
-    __shared__ int4 s_piece[kWaves][PMAX + 2];
-    __shared__ int32_t s_first[kWaves][S + 1];
+    static constexpr int UT = U >= 2 ? 2 : U;
+    static constexpr int EPAD = (EMAX + S * U - 1) / (S * U) * (S * U);
+};
 
-    // Wave-uniform indices, so the work-item records are scalar loads.
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = (int)(threadIdx.x & 63);
-    const int32_t w = (int32_t)(xcd_remap(blockIdx.x, gridDim.x) * kWaves) + wave;
-    const int32_t c0 = w * MERGE;
-    if (c0 >= n_chunks) return;
-    const int32_t c1 = min(n_chunks, c0 + MERGE) - 1;
-    uint32_t* lb = s_brow[wave];
-    uint8_t* lbad = s_bad[wave];
-    float* lv = s_val[wave];
-    int4* lp = s_piece[wave];
-    int32_t* lf = s_first[wave];
+// One wave's LDS: staged entries (B-row byte offsets and values), the piece
+// table with its end sentinels, per-piece "not finite" flags and the streams'
+// first pieces.
+template <int VEC, int LPE, int R, int MERGE>
+struct TileLds {
+    using Sh = TileShape<VEC, LPE, R, MERGE>;
+    __align__(16) float val[Sh::EPAD * Sh::RS];
+    uint32_t brow[Sh::EPAD];
+    int4 piece[Sh::PMAX + 2];
+    int32_t first[Sh::S + 1];
+    uint8_t bad[Sh::PMAX];
+};
+
+// Work items c0 .. c1 (MERGE consecutive items of the view, fewer at the end)
+// on one wave.  BUF: B smaller than 2 GB, read with raw buffer loads at
+// 32-bit byte offsets; otherwise 64-bit addresses from B row indices
+// (LPE = 64 only).
+template <int VEC, int LPE, int R, int MERGE, bool BUF>
+__device__ __forceinline__ void tile_item(
+    int32_t c0, int32_t c1, int lane, TileLds<VEC, LPE, R, MERGE>& L, int32_t O, int32_t ld,
+    int32_t accumulate, uint32_t b_bytes, const int4* __restrict__ chunks,
+    const int4* __restrict__ pieces, const int32_t* __restrict__ ent_brow,
+    const uint16_t* __restrict__ ent_mask, const float* __restrict__ ent_val,
+    const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partials) {
+    using V = typename VecT<VEC>::T;
+    using Sh = TileShape<VEC, LPE, R, MERGE>;
+    constexpr int S = Sh::S;
+    constexpr int RS = Sh::RS;
+    constexpr bool FOLD = tile_dev_folds_brow(R);            // B row inside the values
+    constexpr int DS = tile_dev_stride(R);                   // floats per entry in ent_val
+    constexpr int U = Sh::U;
+    constexpr int UT = Sh::UT;
+    uint32_t* lb = L.brow;
+    uint8_t* lbad = L.bad;
+    float* lv = L.val;
+    int4* lp = L.piece;
+    int32_t* lf = L.first;
+    // The wave's LDS may still be read by its previous work item.
+    wave_sync();
     const int32_t e0 = uniform(chunks[c0].x), ne = uniform(chunks[c1].y) - e0;  // <= EMAX
     const int32_t p0 = uniform(chunks[c0].z), np = uniform(chunks[c1].w) - p0;  // <= PMAX
 
@@ -444,6 +453,32 @@ void vcsr_tile_kernel(
             }
         }
     }
+}
+
+
+// One wave per MERGE consecutive work items of the view.  Up to 3 tile rows
+// (one work item per wave) the register budget is held to 5 waves per SIMD:
+// measured faster than 4 on the banded workload; 6 spills, and so does 5
+// with 4 rows.
+template <int VEC, int LPE, int R, int MERGE, bool BUF>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu((R <= 3 && MERGE == 1) ? 5 : 1, 8)))
+void vcsr_tile_kernel(
+    int32_t n_chunks, int32_t O, int32_t ld, int32_t accumulate, uint32_t b_bytes,
+    const int4* __restrict__ chunks, const int4* __restrict__ pieces,
+    const int32_t* __restrict__ ent_brow, const uint16_t* __restrict__ ent_mask,
+    const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
+    float* __restrict__ partials) {
+    __shared__ TileLds<VEC, LPE, R, MERGE> s_lds[kWaves];
+    // Wave-uniform indices, so the work-item records are scalar loads.
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63);
+    const int32_t w = (int32_t)(xcd_remap(blockIdx.x, gridDim.x) * kWaves) + wave;
+    const int32_t c0 = w * MERGE;
+    if (c0 >= n_chunks) return;
+    tile_item<VEC, LPE, R, MERGE, BUF>(c0, min(n_chunks, c0 + MERGE) - 1, lane, s_lds[wave], O, ld,
+                                       accumulate, b_bytes, chunks, pieces, ent_brow, ent_mask,
+                                       ent_val, B, C, partials);
 }
 
 // Adds the piece partials of one row of a split tile into C; one block per
