@@ -225,7 +225,11 @@ enum {
  * segment-major kernels clear C on the stream first).  tileK applies to the
  * segment-major kernels.  Calls on one format must not overlap in time: the
  * ROW and TILE kernels keep a scratch buffer in the format for the partial
- * sums of very long rows / tiles.
+ * sums of very long rows / tiles.  vcsr_fmt_upload sizes it for the TILE
+ * kernel with tiles of up to 8 rows; the ROW kernel, split 16-row tiles and
+ * unsliced wide launches (B or C not 16-byte aligned, O not a multiple of
+ * 4) grow it on their first call at a wider O, which waits for the stream
+ * and reallocates (spmm_vcsr_noalloc never allocates).
  * No reference counterpart (the reference selects kernels by --algo in
  * src/main.cpp:119-163 and always accumulates). */
 int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,

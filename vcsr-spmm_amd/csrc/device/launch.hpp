@@ -55,6 +55,11 @@ hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, i
                             float* C, int32_t accumulate, float* partials, hipStream_t st);
 int64_t tile_partials_floats(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                              const float* C);
+// Partial-row floats that cover tile_partials_floats when the view's tiles
+// have at most 8 rows, for every O up to 256 and for every wider O whose
+// launches are column slices (16-byte vectors: O a multiple of 4, B and C
+// 16-byte aligned); 0 for 16-row tiles, which are not column-sliced.
+int64_t tile_partials_upload_floats(const DeviceFmt& d);
 // What launch_vcsr_tile launches for these B and C: floats per lane, column
 // slices (one launch each), whether the tiles run on the matrix cores, the
 // reduce launches and the partial-row floats.

@@ -244,6 +244,14 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.tv_split = upload_array(tv.split, st, "upload split tiles");
             d.tv_n_split = (int32_t)(tv.split.size() / 4);
             d.tv_partial_rows = tv.n_partial_rows;
+            const int64_t pf = vcsr::tile_partials_upload_floats(d);
+            if (pf > 0) {
+                hipError_t e = hipMalloc((void**)&d.partials, (size_t)pf * sizeof(float));
+                if (e == hipErrorOutOfMemory)
+                    throw vcsr::Error(VCSR_ENOMEM, "device allocation failed");
+                hip_check(e, "hipMalloc partials");
+                d.partials_floats = pf;
+            }
             // The host vectors above must outlive the copies.
             hip_check(hipStreamSynchronize(st), "upload sync");
         } catch (...) {
@@ -297,18 +305,23 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
         if (kernel == VCSR_KERNEL_AUTO) kernel = VCSR_KERNEL_TILE;
         hipStream_t st = (hipStream_t)stream;
         DeviceFmt& d = const_cast<vcsr_fmt*>(fmt)->dev;
-        const bool row_stationary = kernel == VCSR_KERNEL_ROW || kernel == VCSR_KERNEL_TILE;
-        if (row_stationary && d.partial_rows() > 0 && d.partials_cols < O) {
-            // Scratch for the chunk sums of split rows, kept with the format.
+        // Scratch for the partial sums of split rows / tiles, kept with the
+        // format.  The upload sizes it for the tile kernel with tiles of up
+        // to 8 rows at any O it column-slices (16-byte vectors) or up to 256;
+        // the row kernel, split 16-row tiles and wider unsliced launches grow
+        // it here on first need, which waits for the stream.
+        const int64_t need = kernel == VCSR_KERNEL_TILE
+                                 ? vcsr::tile_partials_floats(fmt->v, d, dB, O, dC)
+                                 : kernel == VCSR_KERNEL_ROW ? (int64_t)d.n_partials * O : 0;
+        if (need > d.partials_floats) {
             hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
             if (d.partials) hip_check(hipFree(d.partials), "hipFree");
             d.partials = nullptr;
-            d.partials_cols = 0;
-            const size_t bytes = (size_t)d.partial_rows() * (size_t)O * sizeof(float);
-            hipError_t e = hipMalloc((void**)&d.partials, bytes);
+            d.partials_floats = 0;
+            hipError_t e = hipMalloc((void**)&d.partials, (size_t)need * sizeof(float));
             if (e == hipErrorOutOfMemory) throw vcsr::Error(VCSR_ENOMEM, "device allocation failed");
             hip_check(e, "hipMalloc partials");
-            d.partials_cols = O;
+            d.partials_floats = need;
         }
         const size_t bytesC = (size_t)fmt->v.M * (size_t)O * sizeof(float);
         run_timed(st, ms, [&]() -> hipError_t {

@@ -849,6 +849,11 @@ int64_t tile_partials_floats(const Vcsr& v, const DeviceFmt& d, const float* B, 
     return (int64_t)d.tv_partial_rows * tile_slicing(v, d, B, O, C).width;
 }
 
+int64_t tile_partials_upload_floats(const DeviceFmt& d) {
+    if (d.tv_R == kTileMmaRows || d.tv_partial_rows == 0) return 0;
+    return (int64_t)d.tv_partial_rows * kTileWideCols;
+}
+
 TilePlan tile_launch_plan(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                           const float* C) {
     TilePlan p;

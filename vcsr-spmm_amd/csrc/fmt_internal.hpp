@@ -50,11 +50,11 @@ struct DeviceFmt {
     int32_t* tv_split = nullptr;        // 4*tv_n_split: row, partial row, stride, pieces
     int32_t tv_n_split = 0;
     int32_t tv_partial_rows = 0;
-    // Partial sums of split rows / tiles: partial_rows() rows of
-    // partials_cols floats, grown on demand.
+    // Partial sums of split rows / tiles (partials_floats floats): sized at
+    // upload for the tile kernel's column slices, grown on demand for the
+    // row kernel and split 16-row tiles.
     float* partials = nullptr;
-    int64_t partials_cols = 0;
-    int32_t partial_rows() const { return n_partials > tv_partial_rows ? n_partials : tv_partial_rows; }
+    int64_t partials_floats = 0;
 };
 
 struct vcsr_coo {
