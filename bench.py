@@ -160,6 +160,8 @@ def main():
                     help="only copy a BYTES buffer device-to-device --steps times (the "
                          "known-size kernel that scales the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.steps < 1 or args.warmup < 0:
+        ap.error("--steps must be at least 1 and --warmup at least 0")
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
