@@ -806,3 +806,38 @@ def test_launch_info_names_what_runs(gpu, orc, st):
     f3.upload(st)
     li3 = f3.launch_info(512)
     assert li3["tile_rows"] == 16 and li3["matrix_cores"] == 1 and li3["column_slices"] == 1
+
+
+
+@pytest.mark.parametrize("where", ["products", "inputs"])
+@pytest.mark.parametrize("kind,tile_rows", [("csr", 0), ("tile", 1), ("tile", 3), ("tile", 16),
+                                            ("row", 0), ("segment", 0), ("mfma", 0)])
+def test_denormals_are_kept(gpu, orc, st, kind, tile_rows, where):
+    """FP32 denormals are kept, as by the reference's CUDA kernels (built
+    without fast-math).  "products": A and B are normal (~2^-64) but every
+    product and partial sum is below the smallest normal, 2^-126;
+    "inputs": B itself is denormal (~2^-140) and A ~2^12.  A flush to zero
+    anywhere gives a relative L2 error near 1; kept denormals leave the
+    north-star bounds met (the denormal grid, 2^-149, is ~2^-20 of these
+    sums).  The naive CSR kernel is also the oracle's FP32 loop bit for
+    bit."""
+    vs = gpu
+    print(f"denormals {where} {kind} R={tile_rows}", flush=True)
+    rng = np.random.default_rng(77 + tile_rows)
+    csr = _block_csr(vs, rng, 12, 16, 160, 4, 16, 0.7)
+    a_exp, b_exp = (-64, -64) if where == "products" else (12, -140)
+    val = (csr.val * np.float32(2.0 ** a_exp)).astype(np.float32)
+    csr = vs.Csr.from_arrays(csr.M, csr.N, csr.row_ptr, csr.col, val)
+    O = 40
+    B = (vs.gen_dense(78, 0, csr.N, O).astype(np.float64) * 2.0 ** b_exp).astype(np.float32)
+    tiny = np.finfo(np.float32).tiny
+    if where == "inputs":
+        assert np.count_nonzero((B != 0) & (np.abs(B) < tiny)) == np.count_nonzero(B)
+    ref32 = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.count_nonzero(ref32) > 0.9 * ref32.size
+    assert np.median(np.abs(ref32[ref32 != 0])) < tiny
+    C = _run(vs, kind, csr, B, st, tile_rows=tile_rows)
+    if kind == "csr":
+        assert np.array_equal(C.view(np.uint32), ref32.view(np.uint32))
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert_within_tolerance(C, ref64, csr.row_ptr, csr.val, B, f"denormal {where} {kind}")
