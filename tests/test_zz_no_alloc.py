@@ -90,3 +90,100 @@ def test_noalloc_refuses_more_scratch_than_it_holds(gpu):
     # A null format is refused the same way as by the other entry points.
     lib = vs.load_library()
     assert lib.spmm_vcsr_noalloc(None, dB.ptr, O, dC.ptr, st.h, 0) == vs.VCSR_EINVAL
+
+
+def _hip_runtime():
+    """The HIP runtime the library is linked against (already loaded with
+    it), for the graph calls; the library itself exports no graph API."""
+    paths = set()
+    with open("/proc/self/maps") as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and "libamdhip64.so" in parts[-1]:
+                paths.add(parts[-1])
+    assert len(paths) == 1, paths
+    hip = ctypes.CDLL(paths.pop())
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    sigs = {"hipStreamBeginCapture": [vp, ctypes.c_int],
+            "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+            "hipGraphGetNodes": [vp, vp, ctypes.POINTER(sz)],
+            "hipGraphNodeGetType": [vp, ctypes.POINTER(ctypes.c_int)],
+            "hipGraphInstantiateWithFlags": [ctypes.POINTER(vp), vp, ctypes.c_ulonglong],
+            "hipGraphLaunch": [vp, vp],
+            "hipGraphExecDestroy": [vp],
+            "hipGraphDestroy": [vp]}
+    for name, args in sigs.items():
+        fn = getattr(hip, name)
+        fn.argtypes, fn.restype = args, ctypes.c_int
+    return hip
+
+
+def test_noalloc_replays_in_a_hip_graph(gpu, orc):
+    """The caller the entry point is for: spmm_vcsr_noalloc captured into a
+    HIP graph (global capture mode, in which an allocation or a
+    synchronising call in the capture fails it) holds kernel nodes only,
+    and every replay gives the eager call's C bit for bit — with C refilled
+    with NaN before each replay and another eager product through the same
+    scratch array between replays."""
+    vs = gpu
+    st = vs.Stream()
+    lib = vs.load_library()
+    print("noalloc graph: 400 rows with split tiles, O=200", flush=True)
+    csr = _long_row_csr(vs, 14, 400, 50000, 9, 2000, 16)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.upload(st)
+    O = 200
+    B = vs.gen_dense(51, 0, csr.N, O)
+    dB = vs.DeviceArray.from_numpy(B, st)
+    d_eager = vs.DeviceArray((csr.M, O), np.float32)
+    d_graph = vs.DeviceArray((csr.M, O), np.float32)
+    # The eager call also looks up the scratch array's address before capture.
+    vs.run_vcsr_spmm_gpu_noalloc(fmt, dB, O, d_eager, st)
+    st.sync()
+    ref = d_eager.numpy(st)
+    want = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert np.linalg.norm(ref - want) <= 1e-5 * np.linalg.norm(want)
+
+    other = _long_row_csr(vs, 15, 120, 20000, 5, 900, 8)
+    ofmt = vs.build_vcsr(other, 4, 64, vs.LAYOUT_S)
+    ofmt.upload(st)
+    oB = vs.DeviceArray.from_numpy(vs.gen_dense(52, 0, other.N, 96), st)
+    oC = vs.DeviceArray((other.M, 96), np.float32)
+    vs.run_vcsr_spmm_gpu_noalloc(ofmt, oB, 96, oC, st)
+    st.sync()
+    oref = oC.numpy(st)
+
+    hip = _hip_runtime()
+    graph, gexec = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipStreamBeginCapture(st.h, 0) == 0  # hipStreamCaptureModeGlobal
+    try:
+        vs.run_vcsr_spmm_gpu_noalloc(fmt, dB, O, d_graph, st)
+    finally:
+        rc_end = hip.hipStreamEndCapture(st.h, ctypes.byref(graph))
+    assert rc_end == 0 and graph.value
+    try:
+        n = ctypes.c_size_t(0)
+        assert hip.hipGraphGetNodes(graph, None, ctypes.byref(n)) == 0
+        nodes = (ctypes.c_void_p * n.value)()
+        assert hip.hipGraphGetNodes(graph, nodes, ctypes.byref(n)) == 0
+        kinds = []
+        for i in range(n.value):
+            t = ctypes.c_int(-1)
+            assert hip.hipGraphNodeGetType(nodes[i], ctypes.byref(t)) == 0
+            kinds.append(t.value)
+        print(f"noalloc graph: {n.value} nodes, types {kinds}", flush=True)
+        assert n.value >= 2 and all(k == 0 for k in kinds)  # tile + reduce kernels only
+        assert hip.hipGraphInstantiateWithFlags(ctypes.byref(gexec), graph, 0) == 0
+        nan = np.full((csr.M, O), np.nan, np.float32)
+        for rep in range(3):
+            print(f"noalloc graph: replay {rep}", flush=True)
+            assert lib.vcsr_memcpy_h2d(d_graph.ptr, nan.ctypes.data, d_graph.nbytes, st.h) == 0
+            vs.run_vcsr_spmm_gpu_noalloc(ofmt, oB, 96, oC, st)
+            assert hip.hipGraphLaunch(gexec, st.h) == 0
+            st.sync()
+            assert np.array_equal(d_graph.numpy(st).view(np.uint32), ref.view(np.uint32)), rep
+            assert np.array_equal(oC.numpy(st).view(np.uint32), oref.view(np.uint32)), rep
+    finally:
+        if gexec.value:
+            hip.hipGraphExecDestroy(gexec)
+        hip.hipGraphDestroy(graph)
