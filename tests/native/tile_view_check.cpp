@@ -110,6 +110,8 @@ static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, in
         const int q = tv.split[4 * i + 1], stride = tv.split[4 * i + 2], n = tv.split[4 * i + 3];
         if (n < 2 || q < 0 || (int64_t)q + (int64_t)(n - 1) * stride >= tv.n_partial_rows)
             return fail("split row partials out of range", M, R);
+        if (i > 0 && n > tv.split[4 * i - 1])
+            return fail("split rows not in decreasing piece count", M, R);
     }
     for (int r = 0; r < M; ++r)
         if (covered[(size_t)r] != 1) return fail("row not covered exactly once", M, R);

@@ -294,6 +294,23 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads, bool fixed) {
         cent += x.nent;
     }
     close_chunk(E);
+    // The reduce kernel takes one split row per block in this order: rows
+    // with the most pieces first, so the longest sums are not the last to
+    // start (cfg3, 2,740 split rows of up to 264 pieces: 1% faster at O = 8
+    // and at O = 128).  Each row's sum does not depend on the order.
+    {
+        const size_t ns = tv.split.size() / 4;
+        std::vector<int32_t> ord(ns);
+        std::iota(ord.begin(), ord.end(), 0);
+        std::stable_sort(ord.begin(), ord.end(), [&](int32_t a, int32_t b) {
+            return tv.split[4 * (size_t)a + 3] > tv.split[4 * (size_t)b + 3];
+        });
+        std::vector<int32_t> sorted(tv.split.size());
+        for (size_t i = 0; i < ns; ++i)
+            std::copy_n(tv.split.begin() + 4 * (ptrdiff_t)ord[i], 4,
+                        sorted.begin() + 4 * (ptrdiff_t)i);
+        tv.split.swap(sorted);
+    }
     tv.n_partial_rows = (int32_t)n_partial;
     return tv;
 }

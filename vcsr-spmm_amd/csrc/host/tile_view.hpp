@@ -93,7 +93,8 @@ struct TileView {
     // Per entry: bit r set where tile row r has the entry's column.
     std::vector<uint16_t> mask;
     // Rows of split tiles, 4 ints each: row, first partial row, stride
-    // between the piece partials of that row, piece count.
+    // between the piece partials of that row, piece count; in decreasing
+    // piece count.
     std::vector<int32_t> split;
     int32_t n_partial_rows = 0;
     int64_t n_entries() const { return (int64_t)brow.size(); }
