@@ -84,6 +84,25 @@ def measured_traffic(config, algo):
         return None
 
 
+def copy_rate_gbs(vs, st, nbytes=512 << 20, reps=10):
+    """Read + write bytes per second of a device-to-device copy of `nbytes`
+    (hipMemcpyAsync), the rate a kernel that only streams bytes through HBM
+    reaches on this GPU; measured in the same run as the SpMM."""
+    src = vs.DeviceArray((nbytes // 4,), np.float32)
+    dst = vs.DeviceArray((nbytes // 4,), np.float32)
+    src.zero(st)
+    for _ in range(2):
+        dst.copy_from(src, st)
+    ev0, ev1 = vs.Event(), vs.Event()
+    ev0.record(st)
+    for _ in range(reps):
+        dst.copy_from(src, st)
+    ev1.record(st)
+    st.sync()
+    ms = ev0.elapsed_ms(ev1) / reps
+    return 2.0 * nbytes / (ms * 1e-3) / 1e9
+
+
 def host_threads():
     """Threads the CPU baseline may use: the cores this process may run on,
     at most 16 (one GPU's share of the GPU box's host) and at most
@@ -394,6 +413,12 @@ def main():
                            "peak": MFMA_FP32_PEAK_TFS, "unit": "TFLOP/s",
                            "frac": round(useful / MFMA_FP32_PEAK_TFS, 4),
                            "traffic": out["roofline"]["traffic"], "bytes_alg": bytes_alg}
+    if out["roofline"]["bound"] == "hbm":
+        # Context for frac: the copy rate is the practical ceiling of any
+        # kernel that moves its bytes through HBM once.
+        copy = copy_rate_gbs(vs, st)
+        out["roofline"]["copy_gbs"] = round(copy, 1)
+        out["roofline"]["frac_of_copy"] = round(achieved / copy, 4)
     if not args.no_cpu_baseline:
         # The oracle's FP32 CSR SpMM (the reference's loop order; the
         # reference has no CPU SpMM of its own) on the same matrix and B:
