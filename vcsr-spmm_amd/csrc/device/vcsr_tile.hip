@@ -649,7 +649,30 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
     };
     const int32_t ng = ne / kTileMmaGroup;
     int32_t g0 = 0;
-    for (; g0 + GU <= ng; g0 += GU) block(std::integral_constant<int, GU>(), g0);
+    if constexpr (SB) {
+        for (; g0 + GU <= ng; g0 += GU) block(std::integral_constant<int, GU>(), g0);
+    } else {
+        // Many waves per SIMD, all resident from the start: the SIMD issues
+        // oldest first, so with equal work the first waves of a SIMD finish
+        // long before its last (cfg5 O = 512: 84 us for the first of 8 against
+        // 134 us for the last, slots busy 78% of the kernel).  The wave's
+        // priority falls with the quarter of its groups done, so lagging
+        // waves issue first: 111-127 us, slots busy 92%, the SpMM 5% faster
+        // (O = 256 and 512).
+        int32_t lvl = 3;
+        __builtin_amdgcn_s_setprio(3);
+        for (; g0 + GU <= ng; g0 += GU) {
+            const int32_t nl = 3 - min(3, (4 * g0) / ng);
+            if (nl != lvl) {
+                lvl = nl;
+                if (lvl == 2) __builtin_amdgcn_s_setprio(2);
+                else if (lvl == 1) __builtin_amdgcn_s_setprio(1);
+                else __builtin_amdgcn_s_setprio(0);
+            }
+            block(std::integral_constant<int, GU>(), g0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+    }
     for (; g0 < ng; ++g0) block(std::integral_constant<int, 1>(), g0);
 
     // This lane holds rows 4*kq + v of the tile, columns col .. col+VEC-1.
