@@ -173,3 +173,21 @@ def test_cli_gpu_algorithms_and_format_file(vs, tmp_path):
             assert "format: saved to" in r.stdout
         if "--load-fmt" in extra:
             assert "format: loaded from" in r.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfg", ["cfg2", "cfg3"])
+def test_cli_all_algorithms_full_size(vs, cfg):
+    """The CLI as the reference's harness drives it, at a headline size:
+    --algo all --check on the full banded / power-law matrix at O = 128.
+    Every algorithm's L2 check against the CPU CSR SpMM (all of C) passes."""
+    if vs.device_count() <= 0:
+        pytest.fail("no GPU visible to the library (gpu tests run on the GPU box)")
+    print(f"cli --gen {cfg} --O 128 --algo all --check", flush=True)
+    r = run_cli(vs, "--gen", cfg, "--O", "128", "--segw", "4", "--bundle", "64", "--tileK", "64",
+                "--algo", "all", "--repeat", "2", "--check")
+    assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-2000:])
+    checks = [line for line in r.stdout.splitlines() if line.startswith("L2 diff")]
+    print("\n".join(checks), flush=True)
+    assert len(checks) >= 5, r.stdout[-3000:]
+    assert all(line.rstrip().endswith("PASS") for line in checks), checks
