@@ -1,7 +1,8 @@
 """bench.py's correctness gate, on the CPU: the whole-C check passes the
 oracle's own FP32 product and fails a C with one element off by more than
 the north-star per-row bound, or with a large relative error; the CPU
-baseline's thread count stays within one GPU's share of the host."""
+baseline's thread count stays within one GPU's share of the host.  On the
+GPU: the fields of its one JSON line."""
 from __future__ import annotations
 
 import importlib.util
@@ -43,3 +44,36 @@ def test_cpu_baseline_threads(bench):
     assert 1 <= n <= 16
     d = bench.host_description()
     assert set(d) == {"cpu_model", "nproc", "affinity_cpus"}
+
+
+@pytest.mark.gpu
+def test_bench_line_contract():
+    """On the GPU: bench.py's one JSON line (short run) carries what the
+    benchmark contract asks for — the BASELINE metric and unit, steps and
+    warm-up as given, a whole-C check that passed, the HBM roofline with
+    live and counter-derived figures, and the CPU baseline on this host."""
+    import json
+    import subprocess
+    import sys
+    print("bench.py --steps 3 --warmup 1 --cpu-seconds 1", flush=True)
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--steps", "3",
+                        "--warmup", "1", "--cpu-seconds", "1"],
+                       capture_output=True, text=True, timeout=600, cwd=ROOT)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    lines = [x for x in r.stdout.splitlines() if x.startswith("{")]
+    assert len(lines) == 1, r.stdout[-2000:]
+    d = json.loads(lines[0])
+    assert d["metric"].startswith("SpMM GFLOP/s") and d["unit"] == "GFLOP/s"
+    assert d["n_gpus"] == 1 and d["steps"] == 3 and d["warmup"] == 1
+    assert d["higher_is_better"] is True and d["dtype"] == "f32" and d["vs_baseline"] is None
+    assert d["value"] > 0 and d["ms_per_step"] > 0 and d["ms_per_step_median"] > 0
+    assert d["config"]["workload"].startswith("cfg2") and "O=128" in d["config"]["workload"]
+    assert d["check"]["rows"] == "all" and d["check"]["result"] == "pass"
+    roof = d["roofline"]
+    assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
+    assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
+    assert roof["traffic"] and roof["traffic"] > 0
+    assert roof["copy_gbs"] > 0 and 0 < roof["frac_of_copy"] < 1.5
+    cpu = d["cpu_baseline"]
+    assert cpu["kind"] == "port" and cpu["value"] > 0 and cpu["cores"] >= 1
+    assert cpu["single_thread"]["cores"] == 1 and cpu["host"]
