@@ -191,3 +191,24 @@ def test_cli_all_algorithms_full_size(vs, cfg):
     print("\n".join(checks), flush=True)
     assert len(checks) >= 5, r.stdout[-3000:]
     assert all(line.rstrip().endswith("PASS") for line in checks), checks
+
+
+def test_integration_shim_compiles(tmp_path):
+    """The C++ shim INTEGRATION.md gives a maintainer of the reference
+    compiles against include/vcsr_spmm.h, with the reference's CSR struct
+    (include/csr.hpp:8-13: M, N, nnz, row_ptr, col, val) and an opaque
+    hipStream_t, as in the reference's translation unit."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    sec = text[text.index("## 2. C++ shim"):]
+    block = sec[sec.index("```cpp") + len("```cpp"):]
+    block = block[:block.index("```")]
+    prelude = ("#include <vector>\n"
+               "struct CSR { int M{0}, N{0}, nnz{0}; std::vector<int> row_ptr; "
+               "std::vector<int> col; std::vector<float> val; };\n"
+               "typedef struct ihipStream_t* hipStream_t;\n")
+    src = tmp_path / "shim.cpp"
+    src.write_text(prelude + block + "\nint main() { return 0; }\n")
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-fsyntax-only", "-I",
+                        os.path.join(ROOT, "include"), str(src)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-3000:]
