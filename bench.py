@@ -10,19 +10,29 @@ kernel (spmm_vcsr_ex, VCSR_KERNEL_AUTO = the tile-stationary VCSR kernel,
 writes every element of C, so a step is its launches alone (one per column
 slice, plus the reduce kernel where tiles are split); the kernels that
 accumulate into C as the reference's do (--algo segment / mfma) get a C
-reset inside the step.  --cols replaces a config's O (column sweeps).  K steps are timed between HIP events after W
-warm-up steps; `value` is 2*nnz*O*K / that time.  `kernel_ms` is the kernel
-alone, K back-to-back launches between events on its stream (the reference
-times kernels only, src/kernels.cu:153-162); the roofline uses it.
-`ms_per_step_median` is the median per-step time of a second pass of K
-steps timed in 10 groups of K/10.  The default kernel's launch shape (tile
-height, column slices, reduce launches) is named in `config`.
+reset inside the step.  --cols replaces a config's O (column sweeps).  K
+steps are timed between HIP events after W warm-up steps; `value` is
+2*nnz*O*K / that time.  `kernel_ms` is the kernel alone, K back-to-back
+launches between events on its stream (the reference times kernels only,
+src/kernels.cu:153-162); the roofline uses it.  `ms_per_step_median` is the
+median per-step time of a second pass of K steps timed in 10 groups of K/10.
+The default kernel's launch shape (tile height, column slices, reduce
+launches) is named in `config`.
+
+The default run also measures, in the same process and each checked over
+all of C, the points the north star's targets name besides the headline
+(`extra`): the power-law workload (config 3) at O = 128 on the default path,
+the naive CSR kernel (src/kernels.cu:15-33) on configs 2 and 3 at O = 128
+with the VCSR / naive speed-up, and the block-sparse workload (config 5) at
+O = 512 with its FP32 MFMA utilisation.  The reference runs every algorithm
+on the same matrix in one process (src/main.cpp:119-163).
 
 Prints ONE JSON line.  Multi-GPU runs are not part of this build.
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -49,6 +59,14 @@ CONFIGS = {
     "cfg5": (5, 512, 16, 16, 64, 2, 1),
 }
 
+# Sources whose code decides the traffic of the dominant (tile) kernel; the
+# counter sets in profiles/traffic.json record their hash.
+TRAFFIC_SOURCES = ("vcsr-spmm_amd/csrc/device/vcsr_tile.hip",
+                   "vcsr-spmm_amd/csrc/device/vecops.hpp",
+                   "vcsr-spmm_amd/csrc/device/common.hpp",
+                   "vcsr-spmm_amd/csrc/host/tile_view.cpp",
+                   "vcsr-spmm_amd/csrc/host/tile_view.hpp")
+
 
 def _load_product():
     import importlib.util
@@ -67,21 +85,35 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def measured_traffic(config, algo):
+def kernel_sources_sha16():
+    """First 16 hex digits of the SHA-256 of TRAFFIC_SOURCES, in order."""
+    h = hashlib.sha256()
+    for rel in TRAFFIC_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(point, algo):
     """HBM-side bytes per SpMM of the dominant kernel, from the committed
-    rocprofv3 counter summary (profiles/traffic.json): FETCH_SIZE and
-    WRITE_SIZE per dispatch, each divided by what the same counter reads per
-    byte for a device-to-device copy of known size, times the kernel's
-    dispatches per SpMM (column slices).  None if absent."""
+    rocprofv3 counter sets (profiles/traffic.json): FETCH_SIZE and WRITE_SIZE
+    per dispatch, each divided by what the same counter reads per byte for a
+    device-to-device copy of known size, times the kernel's dispatches per
+    SpMM (column slices).  Returns (bytes, provenance) — provenance names
+    the commit the counters were taken on and whether this tree's kernel
+    sources are the ones profiled — or (None, None) if absent."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
-        e = t["kernels"][f"{config}/{algo}"]
-        return e.get("launches", 1) * (e["fetch_kib"] * 1024.0 / t["copy_fetch_factor"] +
-                                       e["write_kib"] * 1024.0 / t["copy_write_factor"])
+        e = t["points"][f"{point}/{algo}"]
+        b = e.get("launches", 1) * (e["fetch_kib"] * 1024.0 / t["copy_fetch_factor"] +
+                                    e["write_kib"] * 1024.0 / t["copy_write_factor"])
     except (OSError, KeyError, ValueError, ZeroDivisionError):
-        return None
+        return None, None
+    src = e.get("src_sha16")
+    return b, {"commit": e.get("commit"), "profile": e.get("profile"),
+               "kernel_sources_match": src is not None and src == kernel_sources_sha16()}
 
 
 def copy_rate_gbs(vs, st, nbytes=512 << 20, reps=10):
@@ -160,6 +192,210 @@ def full_check(orc, csr, B, C, nthreads):
     return rel, float(ratio.max() if ratio.size else 0.0)
 
 
+class Workload:
+    """One BASELINE config point's synthetic A (CSR, seed 0), B and C,
+    with B and C resident on the device."""
+
+    def __init__(self, vs, st, point, O=None):
+        cfg, O0, segw, bundle, tileK, layout, dist = CONFIGS[point]
+        self.point, self.O = point, O or O0
+        self.segw, self.bundle, self.tileK, self.layout = segw, bundle, tileK, layout
+        t0 = time.perf_counter()
+        self.csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
+        self.B = vs.gen_dense(cfg, dist, self.csr.N, self.O)
+        log(f"bench: {point} matrix {self.csr.M}x{self.csr.N} nnz={self.csr.nnz} O={self.O} "
+            f"generated in {time.perf_counter() - t0:.2f}s")
+        self.dB = vs.DeviceArray.from_numpy(self.B, st)
+        self.dC = vs.DeviceArray((self.csr.M, self.O), np.float32)
+        c = self.csr
+        self.flop = 2.0 * c.nnz * self.O
+        self.bytes_alg = 4.0 * (c.M + 1) + 8.0 * c.nnz + 4.0 * c.N * self.O + 4.0 * c.M * self.O
+
+
+def make_kernel(vs, st, w, algo, tileK):
+    """The SpMM of `algo` on workload w: returns (kernel(timed) callable,
+    whether a step needs a C reset, the VCSR format or None, format times)."""
+    csr, O = w.csr, w.O
+    if algo in ("rocsparse", "aspt", "csr"):
+        d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
+        d_col = vs.DeviceArray.from_numpy(csr.col, st)
+        d_val = vs.DeviceArray.from_numpy(csr.val, st)
+        keep = (d_rp, d_col, d_val)
+        if algo == "rocsparse":
+            # The vendor baseline (rocSPARSE SpMM, C = A*B), set up once.
+            plan = vs.VendorPlan(csr.M, csr.N, csr.nnz, d_rp, d_col, d_val, w.dB, O, w.dC, st)
+
+            def kernel(timed=False, _k=keep):
+                return plan.run(st, timed=timed)
+        elif algo == "aspt":
+            # Wave-per-row CSR on the plain CSR arrays (overwrites C).
+            def kernel(timed=False, _k=keep):
+                return vs.run_csr_wave_spmm_gpu(csr.M, csr.N, d_rp, d_col, d_val, w.dB, O, w.dC,
+                                                st, timed=timed)
+        else:
+            # Zeroes its own rows (src/kernels.cu:25): no reset needed.
+            def kernel(timed=False, _k=keep):
+                return vs.run_csr_spmm_gpu(csr.M, d_rp, d_col, d_val, w.dB, O, w.dC, st,
+                                           timed=timed)
+        return kernel, False, None, None
+    t0 = time.perf_counter()
+    fmt = vs.build_vcsr(csr, w.segw, w.bundle, w.layout)
+    if algo == "fast":
+        # FastSpMM's layout: fixed 16-row windows of condensed columns.
+        fmt.set_tile_rows(16)
+        fmt.set_tile_windows(True)
+    tb = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    fmt.upload(st)
+    tu = time.perf_counter() - t0
+    tr, tt, te = fmt.tile_info()
+    log(f"bench: VCSR layout={w.layout} groups={fmt.num_groups} slots={fmt.num_slots} "
+        f"build {tb*1e3:.1f} ms upload {tu*1e3:.1f} ms; row-tile view: {tt} tiles of <= {tr} "
+        f"rows, {te} entries ({csr.nnz / max(te, 1):.2f} nonzeros per B-row load)")
+    kern = {"vcsr": vs.KERNEL_AUTO, "tile": vs.KERNEL_TILE, "row": vs.KERNEL_ROW,
+            "segment": vs.KERNEL_SEGMENT, "mfma": vs.KERNEL_MFMA, "fast": vs.KERNEL_TILE}[algo]
+    overwrite = kern in (vs.KERNEL_AUTO, vs.KERNEL_TILE, vs.KERNEL_ROW)
+
+    def kernel(timed=False):
+        return vs.run_vcsr_spmm_gpu_ex(fmt, w.dB, O, tileK, w.dC, st, timed=timed, kernel=kern,
+                                       accumulate=not overwrite)
+    times = {"build_ms": round(tb * 1e3, 2), "upload_ms": round(tu * 1e3, 2),
+             "groups": fmt.num_groups, "slots": fmt.num_slots}
+    return kernel, not overwrite, fmt, times
+
+
+def time_steps(vs, st, w, kernel, needs_reset, steps, warmup, median=True):
+    """W warm-up steps, then K steps between two events on the kernel's
+    stream (total_ms); C after them; the per-step median of a second pass
+    in 10 groups (if `median`); and the kernel alone (kernel_ms: K launches
+    back to back without the reset, which equals total_ms / K when a step
+    needs no reset)."""
+    lib = vs.load_library()
+
+    def step():
+        if needs_reset:
+            w.dC.zero(st)
+        kernel()
+
+    for _ in range(warmup):
+        step()
+    st.sync()
+    ev0, ev1 = vs.Event(), vs.Event()
+    lib.vcsr_device_sync()
+    ev0.record(st)
+    for _ in range(steps):
+        step()
+    ev1.record(st)
+    total_ms = ev0.elapsed_ms(ev1)
+    lib.vcsr_device_sync()
+    C = w.dC.numpy(st)
+    step_ms = None
+    if median:
+        # Per-step durations: a second pass of K steps in (up to) 10 groups
+        # of g consecutive steps with an event between groups, so that an
+        # event record (a few us on this device) is spread over g steps.
+        g = max(1, steps // 10)
+        ngroups = steps // g
+        evs = [vs.Event() for _ in range(ngroups + 1)]
+        lib.vcsr_device_sync()
+        evs[0].record(st)
+        for i in range(ngroups):
+            for _ in range(g):
+                step()
+            evs[i + 1].record(st)
+        step_ms = [evs[i].elapsed_ms(evs[i + 1]) / g for i in range(ngroups)]
+        lib.vcsr_device_sync()
+    if needs_reset:
+        # The kernel alone, K launches back to back (C is left accumulating;
+        # the timing does not depend on its contents).
+        e0, e1 = vs.Event(), vs.Event()
+        lib.vcsr_device_sync()
+        e0.record(st)
+        for _ in range(steps):
+            kernel()
+        e1.record(st)
+        kernel_ms = e0.elapsed_ms(e1) / steps
+        lib.vcsr_device_sync()
+    else:
+        kernel_ms = total_ms / steps
+    return total_ms, kernel_ms, step_ms, C
+
+
+def mfma_report(vs, fmt, algo, w, tileK, kernel_ms):
+    """Matrix-core utilisation of the timed kernel, or None when it does
+    not run on the matrix cores: issued MFMA FLOPs (dense group tiles or
+    16-row tiles, padding included) per kernel time against the dense FP32
+    MFMA peak, the useful share of the issued FLOPs, and the useful rate."""
+    if fmt is None:
+        return None
+    tile_mma = algo in ("vcsr", "tile", "fast") and fmt.tile_info()[0] == 16
+    if not (algo == "mfma" or tile_mma):
+        return None
+    ops, fpo = vs.tile_mfma_work(fmt, w.O) if tile_mma else vs.mfma_work(fmt, w.O, tileK)
+    issued = float(ops) * fpo
+    rate = issued / (kernel_ms * 1e-3) / 1e12
+    useful = w.flop / (kernel_ms * 1e-3) / 1e12
+    return {"instructions": ops, "issued_gflop": round(issued / 1e9, 4),
+            "useful_frac": round(w.flop / issued, 4) if issued else None,
+            "tflops_issued": round(rate, 2), "tflops_useful": round(useful, 2),
+            "peak_tflops": MFMA_FP32_PEAK_TFS,
+            "utilization": round(rate / MFMA_FP32_PEAK_TFS, 4),
+            "useful_frac_of_peak": round(useful / MFMA_FP32_PEAK_TFS, 4)}
+
+
+def extra_point(vs, orc, st, w, algo, steps, warmup, nthreads):
+    """One more point of the same run: the kernel of `algo` on workload w,
+    timed as the headline is (without the median pass) and checked over
+    all of C."""
+    cfg_tileK = CONFIGS[w.point][4]
+    kernel, needs_reset, fmt, _ = make_kernel(vs, st, w, algo, cfg_tileK)
+    total_ms, kernel_ms, _, C = time_steps(vs, st, w, kernel, needs_reset, steps, warmup,
+                                           median=False)
+    rel, worst = full_check(orc, w.csr, w.B, C, nthreads)
+    check = "pass" if rel <= 1e-5 and worst <= 1.0 else "FAIL"
+    log(f"bench: extra {w.point} {algo}: {kernel_ms * 1e3:.2f} us per SpMM, check {check} "
+        f"(rel L2 {rel:.2e}, max-abs / bound {worst:.3f})")
+    achieved = w.bytes_alg / (kernel_ms * 1e-3) / 1e9
+    out = {"workload": f"{w.point}: {w.csr.M}x{w.csr.N} nnz={w.csr.nnz} O={w.O}", "algo": algo,
+           "steps": steps, "warmup": warmup, "kernel_ms": round(kernel_ms, 5),
+           "gflops": round(w.flop / (kernel_ms * 1e-3) / 1e9, 2),
+           "hbm_roofline_frac": round(achieved / HBM_PEAK_GBS, 4),
+           "check": {"rows": "all", "rel_l2": rel, "maxabs_over_bound": round(worst, 4),
+                     "result": check}}
+    if fmt is not None and algo in ("vcsr", "tile"):
+        li = fmt.launch_info(w.O, vs.KERNEL_AUTO)
+        out["timed_kernel"] = ("vcsr_tile_mma_kernel (16-row tiles on FP32 MFMA)"
+                               if li["matrix_cores"] else "vcsr_tile_kernel (row-tile view)")
+        out["reduce_launches"] = li["reduce_launches"]
+    m = mfma_report(vs, fmt, algo, w, cfg_tileK, kernel_ms)
+    if m is not None:
+        out["mfma"] = m
+    return out
+
+
+def north_star_extras(vs, orc, st, head, w2, steps, warmup, nthreads):
+    """The north star's other targets, measured in this run: config 3 at
+    O = 128 on the default path (its HBM roofline fraction), the naive CSR
+    kernel on configs 2 and 3 at O = 128 with the VCSR / naive speed-up
+    (target >= 1.5x), config 5 at O = 512 (FP32 MFMA utilisation)."""
+    ex = {}
+    naive_steps = max(3, steps // 10)
+    ex["cfg2_o128_csr_naive"] = extra_point(vs, orc, st, w2, "csr", naive_steps, 1, nthreads)
+    w3 = Workload(vs, st, "cfg3")
+    ex["cfg3_o128"] = extra_point(vs, orc, st, w3, "vcsr", steps, warmup, nthreads)
+    ex["cfg3_o128_csr_naive"] = extra_point(vs, orc, st, w3, "csr", 3, 1, nthreads)
+    del w3
+    w5 = Workload(vs, st, "cfg5")
+    ex["cfg5_o512"] = extra_point(vs, orc, st, w5, "vcsr", steps, warmup, nthreads)
+    del w5
+    ex["vcsr_over_naive"] = {
+        "cfg2_o128": round(ex["cfg2_o128_csr_naive"]["kernel_ms"] / head["kernel_ms"], 2),
+        "cfg3_o128": round(ex["cfg3_o128_csr_naive"]["kernel_ms"] / ex["cfg3_o128"]["kernel_ms"],
+                           2),
+        "target": 1.5}
+    return ex
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,6 +411,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="wall seconds of each CPU baseline mode (1 thread, all threads)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the extra north-star points the default run measures")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only copy a BYTES buffer device-to-device --steps times (the "
                          "known-size kernel that scales the FETCH_SIZE/WRITE_SIZE counters)")
@@ -208,113 +446,15 @@ def main():
         return
     from oracle import oracle as orc
 
-    cfg, O, segw, bundle, tileK, layout, dist = CONFIGS[args.config]
-    if args.tileK:
-        tileK = args.tileK
-    if args.cols:
-        O = args.cols
-    log(f"bench: {args.config} algo={args.algo} O={O} segw={segw} bundle={bundle} "
+    tileK = args.tileK or CONFIGS[args.config][4]
+    log(f"bench: {args.config} algo={args.algo} O={args.cols or CONFIGS[args.config][1]} "
         f"tileK={tileK} device={vs.device_name()}")
-    t0 = time.perf_counter()
-    csr = vs.coo_to_csr(vs.generate_coo(cfg, 0))
-    B = vs.gen_dense(cfg, dist, csr.N, O)
-    log(f"bench: matrix {csr.M}x{csr.N} nnz={csr.nnz} generated in {time.perf_counter()-t0:.2f}s")
     st = vs.Stream()
-    dB = vs.DeviceArray.from_numpy(B, st)
-    dC = vs.DeviceArray((csr.M, O), np.float32)
-    fmt = None
-    # Kernels that write every C element themselves need no reset per step;
-    # the accumulate-into-C kernels get a C reset inside the timed step.
-    needs_reset = True
-    if args.algo == "rocsparse":
-        # The vendor baseline (rocSPARSE SpMM, C = A*B), set up once.
-        d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
-        d_col = vs.DeviceArray.from_numpy(csr.col, st)
-        d_val = vs.DeviceArray.from_numpy(csr.val, st)
-        plan = vs.VendorPlan(csr.M, csr.N, csr.nnz, d_rp, d_col, d_val, dB, O, dC, st)
-        needs_reset = False
-
-        def kernel(timed=False):
-            return plan.run(st, timed=timed)
-    elif args.algo == "aspt":
-        # Wave-per-row CSR on the plain CSR arrays (overwrites C).
-        d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
-        d_col = vs.DeviceArray.from_numpy(csr.col, st)
-        d_val = vs.DeviceArray.from_numpy(csr.val, st)
-        needs_reset = False
-
-        def kernel(timed=False):
-            return vs.run_csr_wave_spmm_gpu(csr.M, csr.N, d_rp, d_col, d_val, dB, O, dC, st,
-                                            timed=timed)
-    elif args.algo == "csr":
-        d_rp = vs.DeviceArray.from_numpy(csr.row_ptr, st)
-        d_col = vs.DeviceArray.from_numpy(csr.col, st)
-        d_val = vs.DeviceArray.from_numpy(csr.val, st)
-        needs_reset = False  # zeroes its own rows (src/kernels.cu:25)
-
-        def kernel(timed=False):
-            return vs.run_csr_spmm_gpu(csr.M, d_rp, d_col, d_val, dB, O, dC, st, timed=timed)
-    else:
-        t0 = time.perf_counter()
-        fmt = vs.build_vcsr(csr, segw, bundle, layout)
-        if args.algo == "fast":
-            # FastSpMM's layout: fixed 16-row windows of condensed columns.
-            fmt.set_tile_rows(16)
-            fmt.set_tile_windows(True)
-        tb = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        fmt.upload(st)
-        tu = time.perf_counter() - t0
-        log(f"bench: VCSR layout={layout} groups={fmt.num_groups} slots={fmt.num_slots} "
-            f"build {tb*1e3:.1f} ms upload {tu*1e3:.1f} ms")
-        tr, tt, te = fmt.tile_info()
-        log(f"bench: row-tile view: {tt} tiles of <= {tr} rows, {te} entries "
-            f"({csr.nnz / max(te, 1):.2f} nonzeros per B-row load)")
-        kern = {"vcsr": vs.KERNEL_AUTO, "tile": vs.KERNEL_TILE, "row": vs.KERNEL_ROW,
-                "segment": vs.KERNEL_SEGMENT, "mfma": vs.KERNEL_MFMA,
-                "fast": vs.KERNEL_TILE}[args.algo]
-        overwrite = kern in (vs.KERNEL_AUTO, vs.KERNEL_TILE, vs.KERNEL_ROW)
-        needs_reset = not overwrite
-
-        def kernel(timed=False):
-            return vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, tileK, dC, st, timed=timed, kernel=kern,
-                                           accumulate=not overwrite)
-
-    def step():
-        if needs_reset:
-            dC.zero(st)
-        kernel()
-
-    for _ in range(args.warmup):
-        step()
-    st.sync()
-    ev0, ev1 = vs.Event(), vs.Event()
-    lib = vs.load_library()
-    lib.vcsr_device_sync()
-    ev0.record(st)
-    for _ in range(args.steps):
-        step()
-    ev1.record(st)
-    total_ms = ev0.elapsed_ms(ev1)
-    lib.vcsr_device_sync()
-    C = dC.numpy(st)
-
-    # Per-step durations for the median: a second pass of K steps in (up to)
-    # 10 groups of g consecutive steps with an event between groups, so that
-    # an event record (a few us on this device) is spread over g steps; the
-    # median is taken over the groups' per-step times (the headline uses
-    # the first pass).
-    g = max(1, args.steps // 10)
-    ngroups = args.steps // g
-    evs = [vs.Event() for _ in range(ngroups + 1)]
-    lib.vcsr_device_sync()
-    evs[0].record(st)
-    for i in range(ngroups):
-        for _ in range(g):
-            step()
-        evs[i + 1].record(st)
-    step_ms = [evs[i].elapsed_ms(evs[i + 1]) / g for i in range(ngroups)]
-    lib.vcsr_device_sync()
+    w = Workload(vs, st, args.config, args.cols)
+    csr, B, O = w.csr, w.B, w.O
+    kernel, needs_reset, fmt, format_times = make_kernel(vs, st, w, args.algo, tileK)
+    total_ms, kernel_ms, step_ms, C = time_steps(vs, st, w, kernel, needs_reset, args.steps,
+                                                 args.warmup)
 
     # Correctness of the last step of the first pass: every element of C
     # against the oracle (double), the north-star bounds.
@@ -323,32 +463,16 @@ def main():
     check = "pass" if rel <= 1e-5 and worst <= 1.0 else "FAIL"
     log(f"bench: whole-C check vs oracle: rel L2 {rel:.2e}, max-abs / bound {worst:.3f} ({check})")
 
-    # Kernel-only duration: the kernel alone, K launches back to back between
-    # two events on the stream it runs on (C is left accumulating; the
-    # timing does not depend on its contents).  Without a reset in the step
-    # this equals ms_per_step.
-    if needs_reset:
-        e0, e1 = vs.Event(), vs.Event()
-        lib.vcsr_device_sync()
-        e0.record(st)
-        for _ in range(args.steps):
-            kernel()
-        e1.record(st)
-        kernel_ms = e0.elapsed_ms(e1) / args.steps
-        lib.vcsr_device_sync()
-    else:
-        kernel_ms = total_ms / args.steps
-
     config = {"workload": f"{args.config}: {csr.M}x{csr.N} nnz={csr.nnz} O={O}",
-              "algo": args.algo, "segw": segw, "bundle": bundle,
-              "layout": ["H", "S", "TC"][layout] if fmt is not None else "csr",
+              "algo": args.algo, "segw": w.segw, "bundle": w.bundle,
+              "layout": ["H", "S", "TC"][w.layout] if fmt is not None else "csr",
               "step": "C reset + SpMM kernel (C += A*B)" if needs_reset
               else "SpMM kernel writing C = A*B"}
-    if fmt is not None and kern in (vs.KERNEL_AUTO, vs.KERNEL_TILE):
+    if fmt is not None and args.algo in ("vcsr", "tile", "fast"):
         # The tile-stationary kernel walks the row-tile view (derived from the
         # VCSR slots at upload); segw/bundle shape the format it comes from,
         # tileK is the column tile of the segment-major kernels only.
-        li = fmt.launch_info(O, kern)
+        li = fmt.launch_info(O, vs.KERNEL_TILE)
         config.update({
             "timed_kernel": ("vcsr_tile_mma_kernel (16-row tiles on FP32 MFMA)"
                              if li["matrix_cores"] else "vcsr_tile_kernel (row-tile view)"),
@@ -358,16 +482,11 @@ def main():
             "tileK": f"{tileK} (not used by the timed kernel)"})
     elif fmt is not None:
         config["tileK"] = tileK
-    # Host format build (all host threads) and upload, outside the timed
-    # region as in the reference (src/main.cpp:128-149), reported beside it.
-    format_times = ({"build_ms": round(tb * 1e3, 2), "upload_ms": round(tu * 1e3, 2),
-                     "groups": fmt.num_groups, "slots": fmt.num_slots}
-                    if fmt is not None else None)
-    flop = 2.0 * csr.nnz * O
     ms_per_step = total_ms / args.steps
-    value = flop / (ms_per_step * 1e-3) / 1e9
-    bytes_alg = 4.0 * (csr.M + 1) + 8.0 * csr.nnz + 4.0 * csr.N * O + 4.0 * csr.M * O
-    achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
+    value = w.flop / (ms_per_step * 1e-3) / 1e9
+    achieved = w.bytes_alg / (kernel_ms * 1e-3) / 1e9
+    default_o = O == CONFIGS[args.config][1]
+    traffic, provenance = measured_traffic(args.config, args.algo) if default_o else (None, None)
     out = {
         "metric": "SpMM GFLOP/s (2*nnz*O/t) + % of HBM roofline, FP32, O=128, 1xMI355X",
         "value": round(value, 2),
@@ -383,42 +502,41 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": config,
+        # Host format build (all host threads) and upload, outside the timed
+        # region as in the reference (src/main.cpp:128-149), reported beside it.
         "format": format_times,
         "kernel_ms": round(kernel_ms, 5),
-        "kernel_gflops": round(flop / (kernel_ms * 1e-3) / 1e9, 2),
+        "kernel_gflops": round(w.flop / (kernel_ms * 1e-3) / 1e9, 2),
         "check": {"rows": "all", "rel_l2": rel, "maxabs_over_bound": round(worst, 4),
                   "result": check},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": (measured_traffic(args.config, args.algo)
-                                 if O == CONFIGS[args.config][1] else None),
-                     "bytes_alg": bytes_alg},
+                     "traffic": traffic, "traffic_source": provenance,
+                     "bytes_alg": w.bytes_alg},
     }
-    # The tile-stationary kernel runs 16-row tiles on the matrix cores.
-    tile_mma = args.algo in ("vcsr", "tile", "fast") and tr == 16
-    if args.algo == "mfma" or tile_mma:
-        # Matrix-core utilisation: issued MFMA FLOPs (dense group tiles or
-        # 16-row tiles, padding included) per kernel time against the dense
-        # FP32 MFMA peak, and the useful share of the issued FLOPs.  The
-        # roofline that binds is then the FP32 MFMA peak (useful FLOPs).
-        ops, fpo = vs.tile_mfma_work(fmt, O) if tile_mma else vs.mfma_work(fmt, O, tileK)
-        issued = float(ops) * fpo
-        rate = issued / (kernel_ms * 1e-3) / 1e12
-        out["mfma"] = {"instructions": ops, "issued_gflop": round(issued / 1e9, 4),
-                       "useful_frac": round(flop / issued, 4) if issued else None,
-                       "tflops_issued": round(rate, 2), "peak_tflops": MFMA_FP32_PEAK_TFS,
-                       "utilization": round(rate / MFMA_FP32_PEAK_TFS, 4)}
-        useful = flop / (kernel_ms * 1e-3) / 1e12
+    m = mfma_report(vs, fmt, args.algo, w, tileK, kernel_ms)
+    if m is not None:
+        # The roofline that binds is then the FP32 MFMA peak (useful FLOPs).
+        out["mfma"] = m
+        useful = w.flop / (kernel_ms * 1e-3) / 1e12
         out["roofline"] = {"bound": "mfma", "achieved": round(useful, 2),
                            "peak": MFMA_FP32_PEAK_TFS, "unit": "TFLOP/s",
                            "frac": round(useful / MFMA_FP32_PEAK_TFS, 4),
-                           "traffic": out["roofline"]["traffic"], "bytes_alg": bytes_alg}
+                           "traffic": traffic, "traffic_source": provenance,
+                           "bytes_alg": w.bytes_alg}
     if out["roofline"]["bound"] == "hbm":
         # Context for frac: the copy rate is the practical ceiling of any
         # kernel that moves its bytes through HBM once.
         copy = copy_rate_gbs(vs, st)
         out["roofline"]["copy_gbs"] = round(copy, 1)
         out["roofline"]["frac_of_copy"] = round(achieved / copy, 4)
+    checks = [check]
+    if (not args.no_extras and args.config == "cfg2" and args.algo == "vcsr"
+            and args.cols is None):
+        extra_steps = max(5, min(args.steps, 20))
+        out["extra"] = north_star_extras(vs, orc, st, out, w, extra_steps,
+                                         min(args.warmup, 3), nthreads)
+        checks += [v["check"]["result"] for v in out["extra"].values() if "check" in v]
     if not args.no_cpu_baseline:
         # The oracle's FP32 CSR SpMM (the reference's loop order; the
         # reference has no CPU SpMM of its own) on the same matrix and B:
@@ -435,7 +553,7 @@ def main():
                                         f"{med1 * 1e3:.1f} ms)"},
             "host": host_description()}
     print(json.dumps(out), flush=True)
-    if check != "pass":
+    if any(c != "pass" for c in checks):
         sys.exit(1)
 
 

@@ -225,11 +225,13 @@ enum {
  * segment-major kernels clear C on the stream first).  tileK applies to the
  * segment-major kernels.  Calls on one format must not overlap in time: the
  * ROW and TILE kernels keep a scratch buffer in the format for the partial
- * sums of very long rows / tiles.  vcsr_fmt_upload sizes it for the TILE
- * kernel with tiles of up to 8 rows; the ROW kernel, split 16-row tiles and
- * unsliced wide launches (B or C not 16-byte aligned, O not a multiple of
- * 4) grow it on their first call at a wider O, which waits for the stream
- * and reallocates (spmm_vcsr_noalloc never allocates).
+ * sums of very long rows / tiles.  vcsr_fmt_upload sizes it for every O
+ * (a format with split rows or tiles is launched in column slices of at
+ * most 256 columns), so with `ms` NULL a call only enqueues kernels — no
+ * allocation, memset or synchronisation — and can be captured into a HIP
+ * graph.  Only if the upload found too little device memory for that
+ * buffer does the first call that needs it wait for the stream and
+ * allocate it.
  * No reference counterpart (the reference selects kernels by --algo in
  * src/main.cpp:119-163 and always accumulates). */
 int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
@@ -247,7 +249,9 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
  * (spmm_vcsr_ex has no such limit).  Every call on one GPU uses that GPU's
  * array, so calls that overlap in time on one GPU race; its contents are
  * written before they are read, so a call never sees an earlier one's.
- * The format must be uploaded to the current device. */
+ * The format must be uploaded to the current device; the upload looks up
+ * the array's device address, so even the first call may be made under
+ * graph capture. */
 int spmm_vcsr_noalloc(const vcsr_fmt* fmt, const float* dB, int32_t O, float* dC,
                       void* stream, int32_t accumulate);
 

@@ -2,6 +2,7 @@
 oracle (test infrastructure), and the tolerance check of the north star."""
 from __future__ import annotations
 
+import ctypes
 import importlib.util
 import os
 import sys
@@ -113,3 +114,71 @@ def random_csr(rng, M, N, density=0.05, dup_rate=0.0, empty_rows=0.0, max_row=No
     cols = np.array(cols, dtype=np.int32)
     vals = rng.uniform(-1, 1, size=len(rows)).astype(np.float32)
     return rows, cols, vals
+
+
+def hip_runtime():
+    """The HIP runtime the library is linked against (already loaded with
+    it), for the graph-capture calls the tests make; the library itself
+    exports no graph API."""
+    paths = set()
+    with open("/proc/self/maps") as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and "libamdhip64.so" in parts[-1]:
+                paths.add(parts[-1])
+    assert len(paths) == 1, paths
+    hip = ctypes.CDLL(paths.pop())
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    sigs = {"hipStreamBeginCapture": [vp, ctypes.c_int],
+            "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+            "hipGraphGetNodes": [vp, vp, ctypes.POINTER(sz)],
+            "hipGraphNodeGetType": [vp, ctypes.POINTER(ctypes.c_int)],
+            "hipGraphInstantiateWithFlags": [ctypes.POINTER(vp), vp, ctypes.c_ulonglong],
+            "hipGraphLaunch": [vp, vp],
+            "hipGraphExecDestroy": [vp],
+            "hipGraphDestroy": [vp]}
+    for name, args in sigs.items():
+        fn = getattr(hip, name)
+        fn.argtypes, fn.restype = args, ctypes.c_int
+    return hip
+
+
+def capture(hip, stream, enqueue):
+    """Captures what enqueue() puts on `stream` into a HIP graph in global
+    capture mode (an allocation or a synchronising call in the capture makes
+    it fail) and returns (graph, node types); 0 is a kernel node."""
+    graph = ctypes.c_void_p()
+    assert hip.hipStreamBeginCapture(stream.h, 0) == 0  # hipStreamCaptureModeGlobal
+    try:
+        enqueue()
+    finally:
+        rc_end = hip.hipStreamEndCapture(stream.h, ctypes.byref(graph))
+    assert rc_end == 0 and graph.value, f"capture failed: hipStreamEndCapture {rc_end}"
+    n = ctypes.c_size_t(0)
+    assert hip.hipGraphGetNodes(graph, None, ctypes.byref(n)) == 0
+    nodes = (ctypes.c_void_p * n.value)()
+    assert hip.hipGraphGetNodes(graph, nodes, ctypes.byref(n)) == 0
+    kinds = []
+    for i in range(n.value):
+        t = ctypes.c_int(-1)
+        assert hip.hipGraphNodeGetType(nodes[i], ctypes.byref(t)) == 0
+        kinds.append(t.value)
+    return graph, kinds
+
+
+def block_csr(vs, rng, nbr, bh, N, blocks_per_row, bw, keep):
+    """Block-structured matrix: nbr block rows of height bh, each with
+    `blocks_per_row` bh x bw blocks at random block columns; every entry is
+    kept with probability `keep`, so rows of a block row share most but not
+    all of their columns."""
+    rows, cols = [], []
+    nbc = max(1, N // bw)
+    for br in range(nbr):
+        for bc in rng.choice(nbc, size=min(blocks_per_row, nbc), replace=False):
+            rr, cc = np.meshgrid(np.arange(bh) + br * bh, np.arange(bw) + bc * bw, indexing="ij")
+            m = rng.random(rr.shape) < keep
+            rows.append(rr[m]); cols.append(cc[m])
+    rows = np.concatenate(rows).astype(np.int32)
+    cols = np.concatenate(cols).astype(np.int32)
+    vals = rng.uniform(-1, 1, rows.size).astype(np.float32)
+    return vs.coo_to_csr(vs.Coo.from_arrays(nbr * bh, N, rows, cols, vals))

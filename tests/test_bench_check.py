@@ -73,7 +73,32 @@ def test_bench_line_contract():
     assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
     assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
     assert roof["traffic"] and roof["traffic"] > 0
+    assert roof["traffic_source"]["commit"] and "kernel_sources_match" in roof["traffic_source"]
     assert roof["copy_gbs"] > 0 and 0 < roof["frac_of_copy"] < 1.5
     cpu = d["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["value"] > 0 and cpu["cores"] >= 1
     assert cpu["single_thread"]["cores"] == 1 and cpu["host"]
+    # The north star's other points, timed in the same run and checked over
+    # all of C: config 3 at O = 128, naive CSR on configs 2 and 3 with the
+    # VCSR / naive speed-up, config 5 at O = 512 with its MFMA utilisation.
+    ex = d["extra"]
+    for key in ("cfg2_o128_csr_naive", "cfg3_o128", "cfg3_o128_csr_naive", "cfg5_o512"):
+        assert ex[key]["check"]["rows"] == "all" and ex[key]["check"]["result"] == "pass", key
+        assert ex[key]["kernel_ms"] > 0, key
+    assert ex["cfg3_o128"]["workload"].startswith("cfg3") and "O=128" in ex["cfg3_o128"]["workload"]
+    assert 0 < ex["cfg3_o128"]["hbm_roofline_frac"] < 1
+    assert ex["vcsr_over_naive"]["cfg2_o128"] >= 1.5 and ex["vcsr_over_naive"]["cfg3_o128"] >= 1.5
+    m5 = ex["cfg5_o512"]["mfma"]
+    assert "O=512" in ex["cfg5_o512"]["workload"] and 0 < m5["useful_frac_of_peak"] <= 1
+
+
+def test_traffic_provenance(bench, tmp_path, monkeypatch):
+    """roofline.traffic comes with the commit its counters were taken on and
+    whether this tree's tile-kernel sources hash to the recorded value; a
+    point without a counter set gives none."""
+    t, prov = bench.measured_traffic("cfg2", "vcsr")
+    assert t and t > 0 and prov["commit"] and prov["profile"]
+    assert isinstance(prov["kernel_sources_match"], bool)
+    assert bench.measured_traffic("cfg2", "nope") == (None, None)
+    h = bench.kernel_sources_sha16()
+    assert len(h) == 16 and int(h, 16) >= 0

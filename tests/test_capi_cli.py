@@ -101,6 +101,14 @@ def test_python_wrappers_check_buffer_sizes(vs):
             with pytest.raises(vs.VcsrError) as e:
                 run(args)
             assert e.value.code == vs.VCSR_EINVAL
+    # The vendor library is told nnz and reads that many col / val entries:
+    # a larger nnz than the buffers hold (or a negative one) is refused.
+    for nnz in (csr.nnz + 1, -1):
+        for run in (lambda: vs.run_vendor_spmm_gpu(M, N, nnz, rp, col, val, good_b, O, good_c),
+                    lambda: vs.VendorPlan(M, N, nnz, rp, col, val, good_b, O, good_c)):
+            with pytest.raises(vs.VcsrError) as e:
+                run()
+            assert e.value.code == vs.VCSR_EINVAL
 
 
 def run_cli(vs, *args):

@@ -16,7 +16,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import assert_within_tolerance, host_threads, random_csr, row_abs_sums
+from conftest import (assert_within_tolerance, block_csr, host_threads, random_csr,
+                      row_abs_sums)
 
 pytestmark = pytest.mark.gpu
 
@@ -196,6 +197,22 @@ def test_full_size_configs(gpu, orc, st, cfg, O, segw, tileK, layout, kind):
     _colsum_check(csr, B, C)
 
 
+@pytest.mark.parametrize("kind", ["segment", "mfma"])
+def test_cfg5_o512_segment_major_kernels_whole_c(gpu, orc, st, kind):
+    """BASELINE config 5 as it asks: the segmented-streaming kernel and the
+    FP32-MFMA dense-group kernel (src/vcsr_seg.cu:191-231,
+    src/vcsr_tc.cu:197-232) on the full 16K block-sparse matrix at O = 512,
+    layout TC (segw = bundle = 16): every element of C within the north-star
+    bounds of the oracle's double sum, and the column-sum identity."""
+    vs = gpu
+    print(f"cfg5 O=512 {kind}", flush=True)
+    csr = vs.coo_to_csr(vs.generate_coo(5, 0))
+    B = vs.gen_dense(5, 1, csr.N, 512)
+    C = _run(vs, kind, csr, B, st, layout=2, segw=16, bundle=16, tileK=64)
+    _whole_check(orc, csr, B, C, f"cfg5 O=512 {kind}")
+    _colsum_check(csr, B, C)
+
+
 # (cfg, O, segw, layout): every O of the BASELINE configs, cfg4 at both segw.
 BASELINE_POINTS = [(2, 8, 4, 1), (2, 32, 4, 1), (2, 128, 4, 1), (2, 512, 4, 1), (3, 8, 4, 1),
                    (3, 128, 4, 1), (4, 256, 4, 1), (4, 256, 8, 1), (5, 512, 16, 2)]
@@ -301,21 +318,7 @@ def test_full_size_row_kernel(gpu, orc, st, cfg, O, layout, kind):
 
 # ------------------------------------------------------ tile-stationary kernel
 def _block_csr(vs, rng, nbr, bh, N, blocks_per_row, bw, keep):
-    """Block-structured matrix: nbr block rows of height bh, each with
-    `blocks_per_row` bh x bw blocks at random block columns; every entry is
-    kept with probability `keep`, so rows of a block row share most but not
-    all of their columns."""
-    rows, cols = [], []
-    nbc = max(1, N // bw)
-    for br in range(nbr):
-        for bc in rng.choice(nbc, size=min(blocks_per_row, nbc), replace=False):
-            rr, cc = np.meshgrid(np.arange(bh) + br * bh, np.arange(bw) + bc * bw, indexing="ij")
-            m = rng.random(rr.shape) < keep
-            rows.append(rr[m]); cols.append(cc[m])
-    rows = np.concatenate(rows).astype(np.int32)
-    cols = np.concatenate(cols).astype(np.int32)
-    vals = rng.uniform(-1, 1, rows.size).astype(np.float32)
-    return vs.coo_to_csr(vs.Coo.from_arrays(nbr * bh, N, rows, cols, vals))
+    return block_csr(vs, rng, nbr, bh, N, blocks_per_row, bw, keep)
 
 
 @pytest.mark.parametrize("bh,tile_rows", [(2, 0), (3, 0), (4, 0), (8, 0), (16, 0), (3, 1), (3, 2),

@@ -10,6 +10,8 @@ import ctypes
 import numpy as np
 import pytest
 
+from conftest import assert_within_tolerance, block_csr, capture, hip_runtime
+
 pytestmark = pytest.mark.gpu
 
 
@@ -92,32 +94,6 @@ def test_noalloc_refuses_more_scratch_than_it_holds(gpu):
     assert lib.spmm_vcsr_noalloc(None, dB.ptr, O, dC.ptr, st.h, 0) == vs.VCSR_EINVAL
 
 
-def _hip_runtime():
-    """The HIP runtime the library is linked against (already loaded with
-    it), for the graph calls; the library itself exports no graph API."""
-    paths = set()
-    with open("/proc/self/maps") as f:
-        for line in f:
-            parts = line.split()
-            if len(parts) >= 6 and "libamdhip64.so" in parts[-1]:
-                paths.add(parts[-1])
-    assert len(paths) == 1, paths
-    hip = ctypes.CDLL(paths.pop())
-    vp, sz = ctypes.c_void_p, ctypes.c_size_t
-    sigs = {"hipStreamBeginCapture": [vp, ctypes.c_int],
-            "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
-            "hipGraphGetNodes": [vp, vp, ctypes.POINTER(sz)],
-            "hipGraphNodeGetType": [vp, ctypes.POINTER(ctypes.c_int)],
-            "hipGraphInstantiateWithFlags": [ctypes.POINTER(vp), vp, ctypes.c_ulonglong],
-            "hipGraphLaunch": [vp, vp],
-            "hipGraphExecDestroy": [vp],
-            "hipGraphDestroy": [vp]}
-    for name, args in sigs.items():
-        fn = getattr(hip, name)
-        fn.argtypes, fn.restype = args, ctypes.c_int
-    return hip
-
-
 def test_noalloc_replays_in_a_hip_graph(gpu, orc):
     """The caller the entry point is for: spmm_vcsr_noalloc captured into a
     HIP graph (global capture mode, in which an allocation or a
@@ -153,7 +129,7 @@ def test_noalloc_replays_in_a_hip_graph(gpu, orc):
     st.sync()
     oref = oC.numpy(st)
 
-    hip = _hip_runtime()
+    hip = hip_runtime()
     graph, gexec = ctypes.c_void_p(), ctypes.c_void_p()
     assert hip.hipStreamBeginCapture(st.h, 0) == 0  # hipStreamCaptureModeGlobal
     try:
@@ -187,3 +163,95 @@ def test_noalloc_replays_in_a_hip_graph(gpu, orc):
         if gexec.value:
             hip.hipGraphExecDestroy(gexec)
         hip.hipGraphDestroy(graph)
+
+
+@pytest.mark.parametrize("case", ["1-row tiles, two column slices", "split 16-row tiles"])
+def test_noalloc_column_slices_and_16_row_tiles(gpu, orc, case):
+    """The scratch array reused across launches of one call: O = 512 on a
+    format with split 1-row tiles is two column slices, each a tile launch
+    and a reduce through the same array; split 16-row tiles (MFMA) write
+    16 partial rows per piece.  Bit for bit against spmm_vcsr_ex, and the
+    product within the north-star bounds of the oracle."""
+    vs = gpu
+    st = vs.Stream()
+    rng = np.random.default_rng(61)
+    if case.startswith("1-row"):
+        csr, O, rows = _long_row_csr(vs, 16, 300, 30000, 10, 2500, 16), 512, 0
+    else:
+        csr, O, rows = block_csr(vs, rng, 6, 8, 4096, 600, 4, 0.9), 320, 16
+    print(f"noalloc: {case}, O={O}", flush=True)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.set_tile_rows(rows)
+    fmt.upload(st)
+    li = fmt.launch_info(O)
+    assert li["split_rows"] > 0 and li["column_slices"] == 2, li
+    assert li["matrix_cores"] == (rows == 16)
+    B = vs.gen_dense(62, 0, csr.N, O)
+    dB = vs.DeviceArray.from_numpy(B, st)
+    d_ref = vs.DeviceArray((csr.M, O), np.float32)
+    d_got = vs.DeviceArray((csr.M, O), np.float32)
+    nan = np.full((csr.M, O), np.nan, np.float32)
+    lib = vs.load_library()
+    assert lib.vcsr_memcpy_h2d(d_got.ptr, nan.ctypes.data, d_got.nbytes, st.h) == 0
+    vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, 64, d_ref, st, kernel=vs.KERNEL_TILE, accumulate=False)
+    vs.run_vcsr_spmm_gpu_noalloc(fmt, dB, O, d_got, st)
+    st.sync()
+    got, ref = d_got.numpy(st), d_ref.numpy(st)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    want = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    assert_within_tolerance(got, want, csr.row_ptr, csr.val, B, case)
+
+
+_FRESH_CAPTURE = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from conftest import capture, hip_runtime, load_product
+vs = load_product()
+vs.load_library()
+rng = np.random.default_rng(71)
+M, N, O = 200, 30000, 96
+lens = np.where(np.arange(M) % 8 == 3, 1500, 12)
+rows = np.repeat(np.arange(M, dtype=np.int32), lens)
+cols = np.concatenate([rng.choice(N, size=n, replace=False) for n in lens]).astype(np.int32)
+vals = rng.uniform(-1, 1, size=rows.size).astype(np.float32)
+csr = vs.coo_to_csr(vs.Coo.from_arrays(M, N, rows, cols, vals))
+st = vs.Stream()
+fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+fmt.upload(st)
+dB = vs.DeviceArray.from_numpy(vs.gen_dense(72, 0, N, O), st)
+d_graph = vs.DeviceArray((M, O), np.float32)
+d_eager = vs.DeviceArray((M, O), np.float32)
+st.sync()
+hip = hip_runtime()
+# The process's first spmm_vcsr_noalloc call is the captured one.
+graph, kinds = capture(hip, st, lambda: vs.run_vcsr_spmm_gpu_noalloc(fmt, dB, O, d_graph, st))
+assert kinds and all(k == 0 for k in kinds), kinds
+import ctypes
+gexec = ctypes.c_void_p()
+assert hip.hipGraphInstantiateWithFlags(ctypes.byref(gexec), graph, 0) == 0
+assert hip.hipGraphLaunch(gexec, st.h) == 0
+st.sync()
+vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, 64, d_eager, st, kernel=vs.KERNEL_TILE, accumulate=False)
+st.sync()
+g, e = d_graph.numpy(st), d_eager.numpy(st)
+assert np.array_equal(g.view(np.uint32), e.view(np.uint32))
+hip.hipGraphExecDestroy(gexec)
+hip.hipGraphDestroy(graph)
+print("fresh capture OK", len(kinds), "kernel nodes", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_in_a_fresh_process(gpu):
+    """In a process whose first spmm_vcsr_noalloc call is made under graph
+    capture (the upload has already looked up the scratch array's address),
+    the capture holds kernel nodes only and its replay equals the eager
+    spmm_vcsr_ex result bit for bit."""
+    import os
+    import subprocess
+    import sys
+    tests_dir = os.path.dirname(os.path.abspath(__file__))
+    r = subprocess.run([sys.executable, "-c", _FRESH_CAPTURE, tests_dir], capture_output=True,
+                       text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "fresh capture OK" in r.stdout

@@ -464,10 +464,15 @@ def _need_buf(arr, dtype, count, what):
         raise VcsrError(VCSR_EINVAL, f"{what}: {nbytes} bytes, need {int(count) * want.itemsize}")
 
 
-def _need_csr(M, d_rowptr, d_col, d_val):
+def _need_csr(M, d_rowptr, d_col, d_val, nnz=0):
+    """CSR device buffers: row_ptr of M + 1 entries, col and val of equal
+    length and at least `nnz` entries (the vendor library is told nnz and
+    reads that many)."""
+    if nnz < 0:
+        raise VcsrError(VCSR_EINVAL, "negative nnz")
     _need_buf(d_rowptr, np.int32, M + 1, "row_ptr")
-    _need_buf(d_col, np.int32, 0, "col")
-    _need_buf(d_val, np.float32, 0, "val")
+    _need_buf(d_col, np.int32, nnz, "col")
+    _need_buf(d_val, np.float32, nnz, "val")
     if d_col.nbytes // 4 != d_val.nbytes // 4:
         raise VcsrError(VCSR_EINVAL, "col and val lengths differ")
 
@@ -495,7 +500,7 @@ class VendorPlan:
     with its set-up done once."""
 
     def __init__(self, M, N, nnz, d_rowptr, d_col, d_val, dB, O, dC, stream=None):
-        _need_csr(M, d_rowptr, d_col, d_val)
+        _need_csr(M, d_rowptr, d_col, d_val, nnz)
         _need_bc(N, M, O, dB, dC)
         h = C.c_void_p()
         _check(load_library().vcsr_vendor_plan_create(M, N, nnz, d_rowptr.ptr, d_col.ptr,
@@ -520,7 +525,7 @@ class VendorPlan:
 def run_vendor_spmm_gpu(M, N, nnz, d_rowptr, d_col, d_val, dB, O, dC, stream=None, timed=False):
     """One-shot rocSPARSE C = A*B (set-up, SpMM, tear-down, like the
     reference's cuSPARSE wrapper); the SpMM call's ms when timed."""
-    _need_csr(M, d_rowptr, d_col, d_val)
+    _need_csr(M, d_rowptr, d_col, d_val, nnz)
     _need_bc(N, M, O, dB, dC)
     ms = C.c_float(0)
     _check(load_library().spmm_csr_vendor(M, N, nnz, d_rowptr.ptr, d_col.ptr, d_val.ptr, dB.ptr,

@@ -41,10 +41,13 @@ struct MfmaWork {
 MfmaWork mfma_work(const Vcsr& v, int32_t O, int32_t tileK);
 
 // vcsr_rowmajor.hip: row-stationary traversal of the VCSR slots; C = A*B
-// (accumulate = 0) or C += A*B (accumulate = 1).  Needs d.partials sized for
-// O when the format has split rows.
+// (accumulate = 0) or C += A*B (accumulate = 1).  A format with split rows
+// is launched in column slices of at most kRowSliceCols columns, whose
+// partial rows `partials` holds: rowmajor_partials_floats(d, O) floats.
 hipError_t launch_vcsr_rowmajor(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
-                                float* C, int32_t accumulate, hipStream_t st);
+                                float* C, int32_t accumulate, float* partials, hipStream_t st);
+constexpr int32_t kRowSliceCols = 256;
+int64_t rowmajor_partials_floats(const DeviceFmt& d, int32_t O);
 
 // vcsr_tile.hip: tile-stationary traversal of the VCSR slots through the
 // row-tile view; C = A*B (accumulate = 0) or C += A*B (accumulate = 1).
@@ -55,10 +58,9 @@ hipError_t launch_vcsr_tile(const Vcsr& v, const DeviceFmt& d, const float* B, i
                             float* C, int32_t accumulate, float* partials, hipStream_t st);
 int64_t tile_partials_floats(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
                              const float* C);
-// Partial-row floats that cover tile_partials_floats when the view's tiles
-// have at most 8 rows, for every O up to 256 and for every wider O whose
-// launches are column slices (16-byte vectors: O a multiple of 4, B and C
-// 16-byte aligned); 0 for 16-row tiles, which are not column-sliced.
+// Partial-row floats that cover tile_partials_floats for every O, B and C:
+// a view with split tiles is launched in column slices of at most 256
+// columns, and its partial rows are one slice wide.
 int64_t tile_partials_upload_floats(const DeviceFmt& d);
 // What launch_vcsr_tile launches for these B and C: floats per lane, column
 // slices (one launch each), whether the tiles run on the matrix cores, the

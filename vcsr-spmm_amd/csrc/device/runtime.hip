@@ -128,8 +128,9 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxDevices] = {};
 
-// Address of `scratch` on the current device, looked up once per device (on
-// the first call there, with that device current).
+// Address of `scratch` on the current device, looked up once per device
+// (by the first format upload there, with that device current, so that a
+// first spmm_vcsr_noalloc made under graph capture only reads the cache).
 float* scratch_on_current_device() {
     int dev = -1;
     hip_check(hipGetDevice(&dev), "hipGetDevice");
@@ -142,6 +143,21 @@ float* scratch_on_current_device() {
         g_scratch_ptr[dev] = static_cast<float*>(p);
     }
     return g_scratch_ptr[dev];
+}
+
+// Zeroes n floats: C = A*B for the segment-major kernels, which add into
+// C.  A kernel rather than hipMemsetAsync, so that a call captured into a
+// HIP graph records kernel nodes only.
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.f;
+}
+
+hipError_t fill_zero(float* p, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p, n);
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -244,13 +260,23 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.tv_split = upload_array(tv.split, st, "upload split tiles");
             d.tv_n_split = (int32_t)(tv.split.size() / 4);
             d.tv_partial_rows = tv.n_partial_rows;
-            const int64_t pf = vcsr::tile_partials_upload_floats(d);
+            // Partial rows of split tiles (tile kernel) and split rows (row
+            // kernel): both are launched in column slices of at most 256
+            // columns when they have any, so this covers every O and no
+            // SpMM call needs to allocate.  If the device cannot hold it the
+            // format still uploads (kernels without split rows need none)
+            // and spmm_vcsr_ex allocates on its first call that needs it.
+            const int64_t pf = std::max(vcsr::tile_partials_upload_floats(d),
+                                        vcsr::rowmajor_partials_floats(d, vcsr::kRowSliceCols));
             if (pf > 0) {
                 hipError_t e = hipMalloc((void**)&d.partials, (size_t)pf * sizeof(float));
-                if (e == hipErrorOutOfMemory)
-                    throw vcsr::Error(VCSR_ENOMEM, "device allocation failed");
-                hip_check(e, "hipMalloc partials");
-                d.partials_floats = pf;
+                if (e == hipErrorOutOfMemory) {
+                    (void)hipGetLastError();  // not a sticky error: later launches check theirs
+                    d.partials = nullptr;
+                } else {
+                    hip_check(e, "hipMalloc partials");
+                    d.partials_floats = pf;
+                }
             }
             // The host vectors above must outlive the copies.
             hip_check(hipStreamSynchronize(st), "upload sync");
@@ -260,6 +286,15 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
         }
         fmt->dev = d;
         fmt->tv_tiles = tv.n_tiles;
+        // Look up spmm_vcsr_noalloc's scratch array on this device now (it
+        // may load the code object), so that the entry point's calls only
+        // read the cached address.  A failure here is reported by that
+        // entry point, which looks it up again; the upload itself succeeded.
+        try {
+            (void)scratch_on_current_device();
+        } catch (...) {
+            (void)hipGetLastError();
+        }
     });
 }
 
@@ -306,13 +341,15 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
         hipStream_t st = (hipStream_t)stream;
         DeviceFmt& d = const_cast<vcsr_fmt*>(fmt)->dev;
         // Scratch for the partial sums of split rows / tiles, kept with the
-        // format.  The upload sizes it for the tile kernel with tiles of up
-        // to 8 rows at any O it column-slices (16-byte vectors) or up to 256;
-        // the row kernel, split 16-row tiles and wider unsliced launches grow
-        // it here on first need, which waits for the stream.
+        // format and sized at upload for every O (split rows and tiles are
+        // launched in column slices of at most 256 columns), so a call only
+        // enqueues kernels.  Only when the upload could not allocate it
+        // (out of device memory) is it allocated here, on the first call
+        // that needs it, after waiting for the stream.
         const int64_t need = kernel == VCSR_KERNEL_TILE
                                  ? vcsr::tile_partials_floats(fmt->v, d, dB, O, dC)
-                                 : kernel == VCSR_KERNEL_ROW ? (int64_t)d.n_partials * O : 0;
+                                 : kernel == VCSR_KERNEL_ROW ? vcsr::rowmajor_partials_floats(d, O)
+                                                             : 0;
         if (need > d.partials_floats) {
             hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
             if (d.partials) hip_check(hipFree(d.partials), "hipFree");
@@ -323,14 +360,14 @@ int spmm_vcsr_ex(const vcsr_fmt* fmt, const float* dB, int32_t O, int32_t tileK,
             hip_check(e, "hipMalloc partials");
             d.partials_floats = need;
         }
-        const size_t bytesC = (size_t)fmt->v.M * (size_t)O * sizeof(float);
         run_timed(st, ms, [&]() -> hipError_t {
             if (kernel == VCSR_KERNEL_ROW)
-                return vcsr::launch_vcsr_rowmajor(fmt->v, d, dB, O, dC, accumulate, st);
+                return vcsr::launch_vcsr_rowmajor(fmt->v, d, dB, O, dC, accumulate, d.partials,
+                                                  st);
             if (kernel == VCSR_KERNEL_TILE)
                 return vcsr::launch_vcsr_tile(fmt->v, d, dB, O, dC, accumulate, d.partials, st);
-            if (!accumulate && bytesC > 0) {
-                hipError_t e = hipMemsetAsync(dC, 0, bytesC, st);
+            if (!accumulate) {
+                hipError_t e = fill_zero(dC, (int64_t)fmt->v.M * O, st);
                 if (e != hipSuccess) return e;
             }
             if (kernel == VCSR_KERNEL_SEGMENT)

@@ -24,6 +24,8 @@
 // byte offset is the only per-entry address arithmetic (one VALU add) and the
 // hardware range check turns any read past the end of B into zeros.  B
 // buffers of 2 GB or more take the same loop with 64-bit addresses instead.
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 #include "vecops.hpp"
@@ -53,9 +55,11 @@ __device__ __forceinline__ typename VecT<VEC>::T load_b(__amdgpu_buffer_rsrc_t r
 // cross-lane shuffles at the end of each column tile.
 // BUF: raw buffer loads with 32-bit byte offsets (B smaller than 2 GB);
 // otherwise 64-bit addresses with the entry holding the B row index.
+// Columns [0, O) of B and C, whose rows are ld floats apart (ld > O for one
+// column slice); partial rows are O floats.
 template <int VEC, int LPE, bool BUF>
 __global__ __launch_bounds__(256) void vcsr_rowmajor_kernel(
-    int32_t n_items, int32_t O, int32_t bundle, int32_t accumulate, uint32_t b_bytes,
+    int32_t n_items, int32_t O, int32_t ld, int32_t bundle, int32_t accumulate, uint32_t b_bytes,
     const int32_t* __restrict__ row_items, const int4* __restrict__ pair_rec,
     const int32_t* __restrict__ lcol, const float* __restrict__ val,
     const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partials) {
@@ -74,7 +78,7 @@ __global__ __launch_bounds__(256) void vcsr_rowmajor_kernel(
     if (accumulate && p0 == p1) return;  // empty row: nothing to add
 
     // Phase 1: this chunk's entries as (B-row byte offset or row index, value).
-    const uint32_t row_bytes = (uint32_t)O * 4u;
+    const uint32_t row_bytes = (uint32_t)ld * 4u;
     const int32_t np = p1 - p0;  // <= 64 by construction
     int32_t cnt = 0, slot0 = 0, seg = 0;
     if (lane < np) {
@@ -116,7 +120,7 @@ __global__ __launch_bounds__(256) void vcsr_rowmajor_kernel(
             if constexpr (BUF)
                 b = load_b<VEC, true>(rsrc, B, e.x + koff);
             else
-                b = *reinterpret_cast<const V*>(B + (int64_t)e.x * O + koff / 4);
+                b = *reinterpret_cast<const V*>(B + (int64_t)e.x * ld + koff / 4);
         };
         // Full blocks: every sub-group has an entry in each instruction.
         const int32_t nfull = (total / EPI) / U * U;
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(256) void vcsr_rowmajor_kernel(
         for (int sh = LPE; sh < 64; sh <<= 1) acc = add_vec(acc, shfl_xor_vec(acc, sh));
         if (sub != 0 || !kok) continue;
         if (out < 0) {
-            V* dst = reinterpret_cast<V*>(C + (int64_t)row * O + k);
+            V* dst = reinterpret_cast<V*>(C + (int64_t)row * ld + k);
             *dst = accumulate ? add_vec(*dst, acc) : acc;
         } else {
             *reinterpret_cast<V*>(partials + (int64_t)out * O + k) = acc;
@@ -158,7 +162,8 @@ __global__ __launch_bounds__(256) void vcsr_rowmajor_kernel(
 // and 64*VEC-column tile).
 template <int VEC>
 __global__ __launch_bounds__(256) void vcsr_rowmajor_reduce(int32_t n_units, int32_t nkt,
-                                                            int32_t O, int32_t accumulate,
+                                                            int32_t O, int32_t ld,
+                                                            int32_t accumulate,
                                                             const int32_t* __restrict__ split_rows,
                                                             const float* __restrict__ partials,
                                                             float* __restrict__ C) {
@@ -174,40 +179,43 @@ __global__ __launch_bounds__(256) void vcsr_rowmajor_reduce(int32_t n_units, int
     V acc = zero_vec(V());
     for (int32_t q = 0; q < nq; ++q)
         acc = add_vec(acc, *reinterpret_cast<const V*>(partials + (int64_t)(q0 + q) * O + k));
-    V* dst = reinterpret_cast<V*>(C + (int64_t)row * O + k);
+    V* dst = reinterpret_cast<V*>(C + (int64_t)row * ld + k);
     *dst = accumulate ? add_vec(*dst, acc) : acc;
 }
 
 template <int VEC, int LPE, bool BUF>
-hipError_t launch_one(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, float* C,
-                      int32_t accumulate, uint32_t b_bytes, hipStream_t st) {
+hipError_t launch_one(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, int32_t ld,
+                      float* C, int32_t accumulate, uint32_t b_bytes, float* partials,
+                      hipStream_t st) {
     const dim3 grid((unsigned)((d.n_row_items + kWaves - 1) / kWaves)), block(64 * kWaves);
     hipLaunchKernelGGL((vcsr_rowmajor_kernel<VEC, LPE, BUF>), grid, block, 0, st, d.n_row_items,
-                       O, v.bundle, accumulate, b_bytes, d.row_items,
-                       reinterpret_cast<const int4*>(d.pair_rec), d.lcol, d.val, B, C,
-                       d.partials);
+                       O, ld, v.bundle, accumulate, b_bytes, d.row_items,
+                       reinterpret_cast<const int4*>(d.pair_rec), d.lcol, d.val, B, C, partials);
     return hipGetLastError();
 }
 
+// Columns [0, O) of B and C, whose rows are ld floats apart.
 template <int VEC>
-hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, float* C,
-                      int32_t accumulate, hipStream_t st) {
+hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, int32_t ld,
+                      float* C, int32_t accumulate, float* partials, hipStream_t st) {
     if (d.n_row_items > 0) {
-        const uint64_t b_bytes = (uint64_t)v.N * (uint64_t)O * 4u;
+        // Bytes from B to the end of its last row.
+        const uint64_t b_bytes =
+            v.N > 0 ? ((uint64_t)(v.N - 1) * (uint64_t)ld + (uint64_t)O) * 4u : 0u;
         hipError_t e;
         if (b_bytes + 64u * 4u * (uint64_t)VEC >= (uint64_t)kBufferLimit) {
-            e = launch_one<VEC, 64, false>(v, d, B, O, C, accumulate, 0u, st);
+            e = launch_one<VEC, 64, false>(v, d, B, O, ld, C, accumulate, 0u, partials, st);
         } else {
             // Lanes per entry: the smallest power of two covering O.
             const int32_t need = (O + VEC - 1) / VEC;
             const uint32_t bb = (uint32_t)b_bytes;
-            if (need <= 1) e = launch_one<VEC, 1, true>(v, d, B, O, C, accumulate, bb, st);
-            else if (need <= 2) e = launch_one<VEC, 2, true>(v, d, B, O, C, accumulate, bb, st);
-            else if (need <= 4) e = launch_one<VEC, 4, true>(v, d, B, O, C, accumulate, bb, st);
-            else if (need <= 8) e = launch_one<VEC, 8, true>(v, d, B, O, C, accumulate, bb, st);
-            else if (need <= 16) e = launch_one<VEC, 16, true>(v, d, B, O, C, accumulate, bb, st);
-            else if (need <= 32) e = launch_one<VEC, 32, true>(v, d, B, O, C, accumulate, bb, st);
-            else e = launch_one<VEC, 64, true>(v, d, B, O, C, accumulate, bb, st);
+            if (need <= 1) e = launch_one<VEC, 1, true>(v, d, B, O, ld, C, accumulate, bb, partials, st);
+            else if (need <= 2) e = launch_one<VEC, 2, true>(v, d, B, O, ld, C, accumulate, bb, partials, st);
+            else if (need <= 4) e = launch_one<VEC, 4, true>(v, d, B, O, ld, C, accumulate, bb, partials, st);
+            else if (need <= 8) e = launch_one<VEC, 8, true>(v, d, B, O, ld, C, accumulate, bb, partials, st);
+            else if (need <= 16) e = launch_one<VEC, 16, true>(v, d, B, O, ld, C, accumulate, bb, partials, st);
+            else if (need <= 32) e = launch_one<VEC, 32, true>(v, d, B, O, ld, C, accumulate, bb, partials, st);
+            else e = launch_one<VEC, 64, true>(v, d, B, O, ld, C, accumulate, bb, partials, st);
         }
         if (e != hipSuccess) return e;
     }
@@ -216,23 +224,47 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
         const int64_t ru = (int64_t)d.n_split * nkt;
         if (ru > INT32_MAX) return hipErrorInvalidValue;
         hipLaunchKernelGGL(vcsr_rowmajor_reduce<VEC>, dim3((unsigned)((ru + kWaves - 1) / kWaves)),
-                           dim3(64 * kWaves), 0, st, (int32_t)ru, nkt, O, accumulate, d.split_rows,
-                           d.partials, C);
+                           dim3(64 * kWaves), 0, st, (int32_t)ru, nkt, O, ld, accumulate,
+                           d.split_rows, partials, C);
         return hipGetLastError();
     }
     return hipSuccess;
 }
 
+// Column-slice width of a launch over O columns: all of them, or slices of
+// kRowSliceCols when rows are split (their partial rows are one slice wide,
+// so the scratch sized at upload covers every O).
+int32_t row_slice_width(const DeviceFmt& d, int32_t O) {
+    return d.n_split > 0 ? std::min(O, kRowSliceCols) : O;
+}
+
 }  // namespace
 
+int64_t rowmajor_partials_floats(const DeviceFmt& d, int32_t O) {
+    if (O <= 0 || d.n_partials == 0) return 0;
+    return (int64_t)d.n_partials * row_slice_width(d, O);
+}
+
 hipError_t launch_vcsr_rowmajor(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O,
-                                float* C, int32_t accumulate, hipStream_t st) {
+                                float* C, int32_t accumulate, float* partials, hipStream_t st) {
     if (O <= 0 || v.M == 0) return hipSuccess;
     const bool a16 = (((uintptr_t)B | (uintptr_t)C) & 15u) == 0;
     const bool a8 = (((uintptr_t)B | (uintptr_t)C) & 7u) == 0;
-    if (O % 4 == 0 && a16) return launch_vec<4>(v, d, B, O, C, accumulate, st);
-    if (O % 2 == 0 && a8) return launch_vec<2>(v, d, B, O, C, accumulate, st);
-    return launch_vec<1>(v, d, B, O, C, accumulate, st);
+    // Slices start at multiples of kRowSliceCols floats, so they keep the
+    // alignment of B and C.
+    const int32_t width = row_slice_width(d, O);
+    for (int32_t c0 = 0; c0 < O; c0 += width) {
+        const int32_t w = std::min(width, O - c0);
+        hipError_t e;
+        if (w % 4 == 0 && O % 4 == 0 && a16)
+            e = launch_vec<4>(v, d, B + c0, w, O, C + c0, accumulate, partials, st);
+        else if (w % 2 == 0 && O % 2 == 0 && a8)
+            e = launch_vec<2>(v, d, B + c0, w, O, C + c0, accumulate, partials, st);
+        else
+            e = launch_vec<1>(v, d, B + c0, w, O, C + c0, accumulate, partials, st);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace vcsr

@@ -38,8 +38,9 @@
 // the rows the reference's loop reaches.
 //
 // The host launcher runs one launch per column slice of at most 256
-// columns (128 when B is over 512 MB); tiles of 16 rows go to the MFMA
-// kernel further down.
+// columns (128 when B is over 512 MB) for 16-byte vectors, and for any
+// vector width when tiles are split (their partial rows are one slice
+// wide); tiles of 16 rows go to the MFMA kernel further down.
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
@@ -177,8 +178,6 @@ __device__ __forceinline__ void tile_item(
     float* lv = L.val;
     int4* lp = L.piece;
     int32_t* lf = L.first;
-    // The wave's LDS may still be read by its previous work item.
-    wave_sync();
     const int32_t e0 = uniform(chunks[c0].x), ne = uniform(chunks[c1].y) - e0;  // <= EMAX
     const int32_t p0 = uniform(chunks[c0].z), np = uniform(chunks[c1].w) - p0;  // <= PMAX
 
@@ -558,7 +557,9 @@ __global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t O, int32_t ld, i
 // One wave per (piece, column tile of 16*VEC columns).  The grid runs
 // column-tile-major with the XCD-aware block order, so each XCD works on one
 // column range of B at a time and its L2 holds that slice of B (the B rows a
-// block-sparse matrix touches are spread over all of B).
+// block-sparse matrix touches are spread over all of B).  B and C rows are
+// ld floats apart (ld > O for one column slice of a wider product); partial
+// rows are O floats.
 // ---------------------------------------------------------------------------
 typedef float mma_acc4 __attribute__((ext_vector_type(4)));
 constexpr int kMmaWaves = 4;
@@ -575,7 +576,7 @@ __device__ __forceinline__ float vec_part(const typename VecT<VEC>::T& b, int c)
 // fits 8 waves per SIMD.
 template <int VEC, bool BUF, int GU, bool SB>
 __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
-    int32_t n_items, int32_t n_ctiles, int32_t O, int32_t accumulate, uint32_t b_bytes,
+    int32_t n_items, int32_t n_ctiles, int32_t O, int32_t ld, int32_t accumulate, uint32_t b_bytes,
     const int4* __restrict__ chunks, const int4* __restrict__ pieces,
     const int32_t* __restrict__ ent_brow, const uint16_t* __restrict__ ent_mask,
     const float* __restrict__ ent_val, const float* __restrict__ B, float* __restrict__ C,
@@ -596,7 +597,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
 
     // Phase 1: B-row byte offsets (row indices without the buffer path) of
     // the piece's entries; placeholders get "no row".
-    const uint32_t row_bytes = (uint32_t)O * 4u;
+    const uint32_t row_bytes = (uint32_t)ld * 4u;
     for (int32_t i = lane; i < ne; i += 64) {
         const uint32_t br = (uint32_t)ent_brow[e0 + i];
         const bool any = br != (uint32_t)kTileNoEntry;
@@ -618,7 +619,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
         } else {
             const uint32_t br = lb[t];
             if (br == kNoRow || !kok) return zero_vec(V());
-            return *reinterpret_cast<const V*>(B + (int64_t)br * O + col);
+            return *reinterpret_cast<const V*>(B + (int64_t)br * ld + col);
         }
     };
     const float* vp = ent_val + (int64_t)e0 * kTileMmaRows + 4 * lane;
@@ -713,7 +714,7 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
 #pragma unroll
         for (int c = 0; c < VEC; ++c) reinterpret_cast<float*>(&x)[c] = d[c][v];
         if (part < 0) {
-            V* dst = reinterpret_cast<V*>(C + (int64_t)(row0 + r) * O + col);
+            V* dst = reinterpret_cast<V*>(C + (int64_t)(row0 + r) * ld + col);
             store_nt(dst, accumulate ? add_vec(*dst, x) : x);
         } else {
             *reinterpret_cast<V*>(partials + (int64_t)(part + r) * O + col) = x;
@@ -722,10 +723,11 @@ __global__ __launch_bounds__(256) void vcsr_tile_mma_kernel(
 }
 
 template <int VEC, bool BUF, int GU, bool SB>
-void launch_mma_as(const DeviceFmt& d, dim3 grid, int32_t n_ct, int32_t O, int32_t accumulate,
-                   uint32_t b_bytes, const float* B, float* C, float* partials, hipStream_t st) {
+void launch_mma_as(const DeviceFmt& d, dim3 grid, int32_t n_ct, int32_t O, int32_t ld,
+                   int32_t accumulate, uint32_t b_bytes, const float* B, float* C, float* partials,
+                   hipStream_t st) {
     hipLaunchKernelGGL((vcsr_tile_mma_kernel<VEC, BUF, GU, SB>), grid, dim3(64 * kMmaWaves), 0, st,
-                       d.tv_n_chunks, n_ct, O, accumulate, b_bytes,
+                       d.tv_n_chunks, n_ct, O, ld, accumulate, b_bytes,
                        reinterpret_cast<const int4*>(d.tv_chunks),
                        reinterpret_cast<const int4*>(d.tv_pieces), d.tv_brow, d.tv_mask, d.tv_val,
                        B, C, partials);
@@ -733,7 +735,7 @@ void launch_mma_as(const DeviceFmt& d, dim3 grid, int32_t n_ct, int32_t O, int32
 
 template <int VEC, bool BUF>
 void launch_mma_buf(const DeviceFmt& d, dim3 grid, int64_t waves, int32_t n_ct, int32_t O,
-                    int32_t accumulate, uint32_t b_bytes, const float* B, float* C,
+                    int32_t ld, int32_t accumulate, uint32_t b_bytes, const float* B, float* C,
                     float* partials, hipStream_t st) {
     // Few waves per SIMD (cfg5-like matrices at O <= 192): each wave's loads
     // in flight bound the time, so its loads go ahead of its MFMAs; with
@@ -746,25 +748,30 @@ void launch_mma_buf(const DeviceFmt& d, dim3 grid, int64_t waves, int32_t n_ct, 
     // VGPRs); 8 groups measured 1-4% faster than 4 at O = 256 / 512.
     const int64_t simds = 4 * (int64_t)device_cus(d.device);
     if (waves <= simds)
-        launch_mma_as<VEC, BUF, 4, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, partials, st);
+        launch_mma_as<VEC, BUF, 4, true>(d, grid, n_ct, O, ld, accumulate, b_bytes, B, C, partials,
+                                         st);
     else if (waves <= 3 * simds)
-        launch_mma_as<VEC, BUF, 2, true>(d, grid, n_ct, O, accumulate, b_bytes, B, C, partials, st);
+        launch_mma_as<VEC, BUF, 2, true>(d, grid, n_ct, O, ld, accumulate, b_bytes, B, C, partials,
+                                         st);
     else
-        launch_mma_as<VEC, BUF, 8, false>(d, grid, n_ct, O, accumulate, b_bytes, B, C, partials,
-                                          st);
+        launch_mma_as<VEC, BUF, 8, false>(d, grid, n_ct, O, ld, accumulate, b_bytes, B, C,
+                                          partials, st);
 }
 
+// Columns [0, O) of B and C, whose rows are ld floats apart.
 template <int VEC>
-hipError_t launch_mma(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, float* C,
-                      int32_t accumulate, float* partials, hipStream_t st) {
+hipError_t launch_mma(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t O, int32_t ld,
+                      float* C, int32_t accumulate, float* partials, hipStream_t st) {
     const int32_t n_ct = (O + 16 * VEC - 1) / (16 * VEC);
     const int64_t waves = (int64_t)d.tv_n_chunks * n_ct;
     const dim3 grid((unsigned)((waves + kMmaWaves - 1) / kMmaWaves));
-    const uint64_t b_bytes = (uint64_t)v.N * (uint64_t)O * 4u;
+    // Bytes from B to the end of its last row.
+    const uint64_t b_bytes =
+        v.N > 0 ? ((uint64_t)(v.N - 1) * (uint64_t)ld + (uint64_t)O) * 4u : 0u;
     if (b_bytes + 64u * 4u * (uint64_t)VEC >= kBufferLimit)
-        launch_mma_buf<VEC, false>(d, grid, waves, n_ct, O, accumulate, 0u, B, C, partials, st);
+        launch_mma_buf<VEC, false>(d, grid, waves, n_ct, O, ld, accumulate, 0u, B, C, partials, st);
     else
-        launch_mma_buf<VEC, true>(d, grid, waves, n_ct, O, accumulate, (uint32_t)b_bytes, B, C,
+        launch_mma_buf<VEC, true>(d, grid, waves, n_ct, O, ld, accumulate, (uint32_t)b_bytes, B, C,
                                   partials, st);
     return hipGetLastError();
 }
@@ -821,9 +828,7 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
             case 4: e = launch_r<VEC, 4>(d, B, O, ld, C, accumulate, b_bytes, partials, st); break;
             case 8: e = launch_r<VEC, 8>(d, B, O, ld, C, accumulate, b_bytes, partials, st); break;
             case kTileMmaRows:
-                // 16-row tiles are never column-sliced: their rows are O apart.
-                if (ld != O) return hipErrorInvalidValue;
-                e = launch_mma<VEC>(v, d, B, O, C, accumulate, partials, st);
+                e = launch_mma<VEC>(v, d, B, O, ld, C, accumulate, partials, st);
                 break;
             default: return hipErrorInvalidValue;
         }
@@ -874,6 +879,10 @@ static TileSlicing tile_slicing(const Vcsr& v, const DeviceFmt& d, const float* 
         if ((uint64_t)v.N * (uint64_t)O * 4u > kTileSliceBytes) ts.width = std::min(O, kTileSliceCols);
         else ts.width = std::min(O, kTileWideCols);
     }
+    // Split tiles write partial rows one slice wide: whatever the tile
+    // height and vector width, a launch then covers at most the 256 columns
+    // the upload sizes the partial rows for, so no O needs more scratch.
+    if (d.tv_partial_rows > 0) ts.width = std::min(ts.width, kTileWideCols);
     return ts;
 }
 
@@ -884,7 +893,6 @@ int64_t tile_partials_floats(const Vcsr& v, const DeviceFmt& d, const float* B, 
 }
 
 int64_t tile_partials_upload_floats(const DeviceFmt& d) {
-    if (d.tv_R == kTileMmaRows || d.tv_partial_rows == 0) return 0;
     return (int64_t)d.tv_partial_rows * kTileWideCols;
 }
 
