@@ -51,8 +51,9 @@ struct DeviceFmt {
     int32_t tv_n_split = 0;
     int32_t tv_partial_rows = 0;
     // Partial sums of split rows / tiles (partials_floats floats): sized at
-    // upload for the tile kernel's column slices, grown on demand for the
-    // row kernel and split 16-row tiles.
+    // upload for every O (split rows and tiles are launched in column slices
+    // of at most 256 columns); allocated by the first call that needs it
+    // only when the upload ran out of device memory.
     float* partials = nullptr;
     int64_t partials_floats = 0;
 };
