@@ -626,6 +626,68 @@ def test_unaligned_b_and_c(gpu, orc, st, kind, off):
     assert_within_tolerance(dC.numpy(), ref64, csr.row_ptr, csr.val, B, f"{kind} off{off}")
 
 
+@pytest.mark.parametrize("kind,tile_rows", [("row", 0), ("tile", 1), ("tile", 3), ("tile", 16)])
+@pytest.mark.parametrize("off,O", [(4, 301), (8, 522), (0, 301)])
+def test_split_rows_in_column_slices_at_any_width(gpu, orc, st, kind, tile_rows, off, O):
+    """Formats with split rows (row kernel) or split tiles (tile kernel,
+    VALU and 16-row MFMA) run in column slices of at most 256 columns, whose
+    partial rows are one slice wide, also when O is not a multiple of 4 or
+    B and C are only 4- or 8-byte aligned (1- or 2-float lanes, which used
+    to run unsliced): every element of C against the oracle, in both C
+    modes, the second call reusing the scratch."""
+    vs = gpu
+    rng = np.random.default_rng(off * 1000 + O + tile_rows)
+    csr = _block_csr(vs, rng, 6, 8, 4096, 600, 4, 0.9)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.set_tile_rows(tile_rows)
+    fmt.upload(st)
+    kernel = vs.KERNEL_ROW if kind == "row" else vs.KERNEL_TILE
+    if kind == "tile":
+        li = fmt.launch_info(O, kernel)
+        assert li["split_rows"] > 0 and li["column_slices"] == -(-O // 256), li
+    B = vs.gen_dense(O + off, 0, csr.N, O)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    C0 = rng.uniform(-1, 1, size=(csr.M, O)).astype(np.float32)
+    dB = _Shifted(vs, B, off, st)
+    for accumulate in (False, True):
+        dC = _Shifted(vs, C0, off, st)
+        vs.run_vcsr_spmm_gpu_ex(fmt, dB, O, 64, dC, st, timed=True, kernel=kernel,
+                                accumulate=accumulate)
+        got = dC.numpy()
+        if accumulate:
+            got = got - C0
+        assert_within_tolerance(got, ref64, csr.row_ptr, csr.val, B,
+                                f"{kind} R{tile_rows} off{off} O{O} acc{accumulate}")
+
+
+@pytest.mark.parametrize("tile_rows", [1, 16])
+def test_nonfinite_b_with_split_tiles_in_column_slices(gpu, orc, st, tile_rows):
+    """Inf and NaN in B reach exactly the reference's C entries when the
+    tiles are split into pieces (partial rows summed by the reduce kernel)
+    and the launch is cut into column slices: O = 300, 16-row MFMA tiles and
+    1-row tiles."""
+    vs = gpu
+    rng = np.random.default_rng(17 + tile_rows)
+    csr = _block_csr(vs, rng, 6, 8, 4096, 600, 4, 0.9)
+    O = 300
+    B = vs.gen_dense(23, 0, csr.N, O)
+    B[5, 3] = np.inf
+    B[17, :] = np.nan
+    B[40, 270] = -np.inf
+    ref = orc.spmm_f32(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.set_tile_rows(tile_rows)
+    fmt.upload(st)
+    li = fmt.launch_info(O)
+    assert li["split_rows"] > 0 and li["column_slices"] == 2, li
+    C = _ex(vs, fmt, B, np.zeros((csr.M, O), np.float32), st, vs.KERNEL_TILE, False)
+    assert np.array_equal(np.isnan(C), np.isnan(ref))
+    assert np.array_equal(np.isposinf(C), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(C), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    assert np.allclose(C[fin], ref[fin], rtol=1e-5, atol=1e-4)
+
+
 def test_loaded_format_computes_the_same(gpu, orc, st, tmp_path):
     """A format saved and loaded back (with its tile settings) uploads and
     gives bit-identical results to the format it was saved from."""
