@@ -23,9 +23,10 @@ The default run also measures, in the same process and each checked over
 all of C, the points the north star's targets name besides the headline
 (`extra`): the power-law workload (config 3) at O = 128 on the default path,
 the naive CSR kernel (src/kernels.cu:15-33) on configs 2 and 3 at O = 128
-with the VCSR / naive speed-up, and the block-sparse workload (config 5) at
-O = 512 with its FP32 MFMA utilisation.  The reference runs every algorithm
-on the same matrix in one process (src/main.cpp:119-163).
+with the VCSR / naive speed-up, the block-sparse workload (config 5) at
+O = 512 with its FP32 MFMA utilisation, and rocSPARSE on the headline
+workload (the reference's cuSPARSE comparison).  The reference runs every
+algorithm on the same matrix in one process (src/main.cpp:119-163).
 
 Prints ONE JSON line.  Multi-GPU runs are not part of this build.
 """
@@ -377,10 +378,13 @@ def north_star_extras(vs, orc, st, head, w2, steps, warmup, nthreads):
     """The north star's other targets, measured in this run: config 3 at
     O = 128 on the default path (its HBM roofline fraction), the naive CSR
     kernel on configs 2 and 3 at O = 128 with the VCSR / naive speed-up
-    (target >= 1.5x), config 5 at O = 512 (FP32 MFMA utilisation)."""
+    (target >= 1.5x), config 5 at O = 512 (FP32 MFMA utilisation); and the
+    vendor SpMM (rocSPARSE, the counterpart of the reference's cuSPARSE
+    column, src/kernels.cu:169-235) on the headline workload."""
     ex = {}
     naive_steps = max(3, steps // 10)
     ex["cfg2_o128_csr_naive"] = extra_point(vs, orc, st, w2, "csr", naive_steps, 1, nthreads)
+    ex["cfg2_o128_rocsparse"] = extra_point(vs, orc, st, w2, "rocsparse", steps, warmup, nthreads)
     w3 = Workload(vs, st, "cfg3")
     ex["cfg3_o128"] = extra_point(vs, orc, st, w3, "vcsr", steps, warmup, nthreads)
     ex["cfg3_o128_csr_naive"] = extra_point(vs, orc, st, w3, "csr", 3, 1, nthreads)
@@ -393,6 +397,8 @@ def north_star_extras(vs, orc, st, head, w2, steps, warmup, nthreads):
         "cfg3_o128": round(ex["cfg3_o128_csr_naive"]["kernel_ms"] / ex["cfg3_o128"]["kernel_ms"],
                            2),
         "target": 1.5}
+    ex["vcsr_over_rocsparse"] = {
+        "cfg2_o128": round(ex["cfg2_o128_rocsparse"]["kernel_ms"] / head["kernel_ms"], 2)}
     return ex
 
 

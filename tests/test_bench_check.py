@@ -82,12 +82,14 @@ def test_bench_line_contract():
     # all of C: config 3 at O = 128, naive CSR on configs 2 and 3 with the
     # VCSR / naive speed-up, config 5 at O = 512 with its MFMA utilisation.
     ex = d["extra"]
-    for key in ("cfg2_o128_csr_naive", "cfg3_o128", "cfg3_o128_csr_naive", "cfg5_o512"):
+    for key in ("cfg2_o128_csr_naive", "cfg2_o128_rocsparse", "cfg3_o128", "cfg3_o128_csr_naive",
+                "cfg5_o512"):
         assert ex[key]["check"]["rows"] == "all" and ex[key]["check"]["result"] == "pass", key
         assert ex[key]["kernel_ms"] > 0, key
     assert ex["cfg3_o128"]["workload"].startswith("cfg3") and "O=128" in ex["cfg3_o128"]["workload"]
     assert 0 < ex["cfg3_o128"]["hbm_roofline_frac"] < 1
     assert ex["vcsr_over_naive"]["cfg2_o128"] >= 1.5 and ex["vcsr_over_naive"]["cfg3_o128"] >= 1.5
+    assert ex["vcsr_over_rocsparse"]["cfg2_o128"] > 0
     m5 = ex["cfg5_o512"]["mfma"]
     assert "O=512" in ex["cfg5_o512"]["workload"] and 0 < m5["useful_frac_of_peak"] <= 1
 
