@@ -51,6 +51,14 @@ class _Coo(C.Structure):
                 ("vals", C.POINTER(C.c_float))]
 
 
+class _Cst(C.Structure):
+    _fields_ = [("M", C.c_int), ("N", C.c_int), ("num_windows", C.c_int), ("num_tcb", C.c_int),
+                ("num_entries", C.c_int), ("window_off", C.POINTER(C.c_int)),
+                ("tcb_col_off", C.POINTER(C.c_int)), ("tcb_row_off", C.POINTER(C.c_int)),
+                ("col_idx", C.POINTER(C.c_ubyte)), ("value", C.POINTER(C.c_float)),
+                ("tcb2b", C.POINTER(C.c_int))]
+
+
 def _take(lib_free, ptr, n, dtype):
     out = (np.ctypeslib.as_array(ptr, shape=(n,)).astype(dtype, copy=True)
            if n else np.zeros(0, dtype=dtype))
@@ -90,6 +98,8 @@ def oracle_lib():
         lib.orc_spmm_f64_mt.restype = None
         lib.orc_vcsr_apply.argtypes = [C.c_int] * 5 + [C.c_void_p] * 7 + [C.c_int, C.c_void_p]
         lib.orc_vcsr_apply.restype = None
+        lib.orc_build_cst.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.POINTER(_Cst)]
         _orc = lib
     return _orc
 
@@ -206,6 +216,26 @@ def vcsr_apply(M, N, fmt, B):
                        _p(a["group_ptr"]), _p(a["group_depth"]), _p(a["group_seg_base"]),
                        _p(a["group_rows"]), _p(a["lcol"]), _p(a["val"]), _p(B), O, _p(out))
     return out
+
+
+def build_cst(M, N, row_ptr, col, val):
+    """FastSpMM's condensed sparse tiles (16-row windows, 16-column TCBs) as a
+    dict of arrays: window_off (W+1), tcb_col_off (T+1), tcb_row_off (17 T,
+    absolute entry numbers), col_idx (uint8), value (float32), tcb2b (16 T)."""
+    lib = oracle_lib()
+    row_ptr, col = np.ascontiguousarray(row_ptr, np.int32), np.ascontiguousarray(col, np.int32)
+    val = np.ascontiguousarray(val, np.float32)
+    s = _Cst()
+    if lib.orc_build_cst(M, N, _p(row_ptr), _p(col), _p(val), C.byref(s)) != 0:
+        raise RuntimeError("oracle build_cst: " + lib.orc_last_error().decode())
+    T, E, f = s.num_tcb, s.num_entries, lib.orc_free
+    return {"num_windows": s.num_windows, "num_tcb": T,
+            "window_off": _take(f, s.window_off, s.num_windows + 1, np.int32),
+            "tcb_col_off": _take(f, s.tcb_col_off, T + 1, np.int32),
+            "tcb_row_off": _take(f, s.tcb_row_off, 17 * T, np.int32),
+            "col_idx": _take(f, s.col_idx, E, np.uint8),
+            "value": _take(f, s.value, E, np.float32),
+            "tcb2b": _take(f, s.tcb2b, 16 * T, np.int32)}
 
 
 # -------------------------------------------------------------- reference

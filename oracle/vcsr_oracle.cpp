@@ -11,6 +11,7 @@
 //   orc_build_h          include/vcsr.hpp:25-109      (layout H)
 //   orc_build_s          src/vcsr_seg.cu:24-113       (layout S; = vcsr_opt.cu:23-101)
 //   orc_build_tc         src/vcsr_tc.cu:26-106        (layout S with segw=16, bundle=16)
+//   orc_build_cst        src/fastspmm.cu:129-251      (FastSpMM condensed tiles)
 //   orc_spmm_f32         src/kernels.cu:25-32 loop order (row; p ascending; k inner; FMA)
 //   orc_spmm_f64         same sum in double (checker only)
 //   orc_spmm_f{32,64}_mt the same two over row ranges on several threads
@@ -237,6 +238,70 @@ Fmt build_s(const Csr& csr, int segw, int bundle) {
     return F;
 }
 
+// FastSpMM's condensed sparse tiles (src/fastspmm.cu:129-251; its header
+// fastspmm.hpp is missing, and the window and block widths are 16 because
+// the kernel's WMMA tiles are 16 x 16, fastspmm.cu:44-48,103).
+struct Cst {
+    int M = 0, N = 0, num_windows = 0, num_tcb = 0;
+    std::vector<int> window_off;    // rowWindowOffset: first TCB of each window, + end
+    std::vector<int> tcb_col_off;   // tcbColOffset: first entry of each TCB, + end
+    std::vector<int> tcb_row_off;   // tcbRowOffset: 17 per TCB (uint16_t there, see below)
+    std::vector<uint8_t> col_idx;   // tcbColIndex: column inside the TCB, 0..15
+    std::vector<float> value;       // tcbValue (__half there, see below)
+    std::vector<int> tcb2b;         // tcb2B: 16 per TCB, B row or -1
+};
+
+// Per window of 16 rows: the distinct columns of its rows in increasing
+// order (:160-167; a window without any adds no TCB, :169-171); column i of
+// that list belongs to TCB i / 16 at position i % 16 (:174-180, :194-196);
+// each TCB lists, row by row, the row's nonzeros whose column it holds, in
+// CSR order (:188-201, :215-224), with the running entry count before each
+// row and after the last (:216, :225, :228), and its 16 columns (-1 past the
+// window's last, :231-235).  The row offsets are absolute entry numbers; the
+// reference stores them as uint16_t (:216, :225), which wraps once a matrix
+// has more than 65535 entries, while its kernel subtracts the TCB's 32-bit
+// first entry from them (fastspmm.cu:61-71): this restatement keeps them in
+// int.  Values stay float: the reference rounds them to half (:221), its
+// arithmetic precision, not part of the layout.
+Cst build_cst(const Csr& csr) {
+    constexpr int kWin = 16, kTcbW = 16;
+    Cst s;
+    s.M = csr.M;
+    s.N = csr.N;
+    s.num_windows = (csr.M + kWin - 1) / kWin;
+    s.window_off.push_back(0);
+    s.tcb_col_off.push_back(0);
+    for (int w = 0; w < s.num_windows; ++w) {
+        const int r0 = w * kWin, r1 = std::min(csr.M, r0 + kWin);
+        std::vector<int> cols(csr.col.begin() + csr.row_ptr[r0], csr.col.begin() + csr.row_ptr[r1]);
+        std::sort(cols.begin(), cols.end());
+        cols.erase(std::unique(cols.begin(), cols.end()), cols.end());
+        const int ntcb = ((int)cols.size() + kTcbW - 1) / kTcbW;
+        for (int t = 0; t < ntcb; ++t) {
+            for (int lr = 0; lr < kWin; ++lr) {
+                s.tcb_row_off.push_back((int)s.col_idx.size());
+                if (r0 + lr >= r1) continue;
+                for (int p = csr.row_ptr[r0 + lr]; p < csr.row_ptr[r0 + lr + 1]; ++p) {
+                    const int i = (int)(std::lower_bound(cols.begin(), cols.end(), csr.col[p]) -
+                                        cols.begin());
+                    if (i / kTcbW != t) continue;
+                    s.col_idx.push_back((uint8_t)(i % kTcbW));
+                    s.value.push_back(csr.val[p]);
+                }
+            }
+            s.tcb_row_off.push_back((int)s.col_idx.size());
+            s.tcb_col_off.push_back((int)s.col_idx.size());
+            for (int j = 0; j < kTcbW; ++j) {
+                const int i = t * kTcbW + j;
+                s.tcb2b.push_back(i < (int)cols.size() ? cols[(size_t)i] : -1);
+            }
+        }
+        s.num_tcb += ntcb;
+        s.window_off.push_back(s.num_tcb);
+    }
+    return s;
+}
+
 thread_local std::string g_err;
 
 template <class T>
@@ -343,6 +408,43 @@ int orc_build(int M, int N, const int* row_ptr, const int* col, const float* val
         out->lcol = dup(F.lcol);
         out->val = dup(F.val);
         out->segment_group_start = dup(F.segment_group_start);
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 1;
+    }
+}
+
+typedef struct {
+    int M, N, num_windows, num_tcb, num_entries;
+    int *window_off, *tcb_col_off, *tcb_row_off;
+    unsigned char* col_idx;
+    float* value;
+    int* tcb2b;
+} orc_cst;
+
+int orc_build_cst(int M, int N, const int* row_ptr, const int* col, const float* val,
+                  orc_cst* out) {
+    try {
+        Csr c;
+        c.M = M;
+        c.N = N;
+        c.nnz = row_ptr[M];
+        c.row_ptr.assign(row_ptr, row_ptr + M + 1);
+        c.col.assign(col, col + c.nnz);
+        c.val.assign(val, val + c.nnz);
+        Cst s = build_cst(c);
+        out->M = s.M;
+        out->N = s.N;
+        out->num_windows = s.num_windows;
+        out->num_tcb = s.num_tcb;
+        out->num_entries = (int)s.col_idx.size();
+        out->window_off = dup(s.window_off);
+        out->tcb_col_off = dup(s.tcb_col_off);
+        out->tcb_row_off = dup(s.tcb_row_off);
+        out->col_idx = dup(s.col_idx);
+        out->value = dup(s.value);
+        out->tcb2b = dup(s.tcb2b);
         return 0;
     } catch (const std::exception& e) {
         g_err = e.what();

@@ -12,6 +12,10 @@
 //    piece);
 //  * keep each tile's entries sorted by column (the B rows are walked in
 //    the order of the row's nonzeros).
+// With fixed 16-row windows (the FastSpMM layout) the view must also be the
+// oracle's restatement of FastSpMM's condensed sparse tiles
+// (oracle/vcsr_oracle.cpp orc_build_cst, src/fastspmm.cu:129-251), linked in
+// from the oracle's source: see check_cst.
 // Exit status 0 and "ALL OK" when every case passes.
 #include <algorithm>
 #include <cmath>
@@ -25,9 +29,145 @@
 
 using namespace vcsr;
 
+// The oracle's C interface for the condensed tiles (oracle/vcsr_oracle.cpp).
+extern "C" {
+typedef struct {
+    int M, N, num_windows, num_tcb, num_entries;
+    int *window_off, *tcb_col_off, *tcb_row_off;
+    unsigned char* col_idx;
+    float* value;
+    int* tcb2b;
+} orc_cst;
+int orc_build_cst(int M, int N, const int* row_ptr, const int* col, const float* val,
+                  orc_cst* out);
+void orc_free(void* p);
+}
+
 static int fail(const char* what, int M, int R) {
     std::printf("FAIL %s (M=%d R=%d)\n", what, M, R);
     return 1;
+}
+
+static bool same_bits(float a, float b) { return std::memcmp(&a, &b, sizeof a) == 0; }
+
+// The fixed-window view at tile height 16 against FastSpMM's condensed
+// sparse tiles.  Window w (rows 16w ..) is tile w of the view.  Where no row
+// of the window holds a column twice:
+//  * its entries are the window's TCBs, 16 per TCB: entry 16t + j reads the
+//    B row tcb2B[16t + j], and TCB padding (-1) is a placeholder entry;
+//  * row r of the window has a value in entry 16t + j exactly where TCB t
+//    lists local column j for local row r, with the same value.
+// A window without nonzeros has no TCB and one group of 16 placeholder
+// entries in the view (a 16-row tile always has a whole entry group).  A row
+// that holds a column twice has both entries in one TCB cell (the reference
+// kernel keeps one of them, fastspmm.cu:74-79) and two entries in the view;
+// there the view's (row, B row, value) multiset must equal the CST's, and
+// its distinct B rows the window's column list.
+static int check_cst(const Csr& csr, int segw, int bundle, int layout) {
+    const int M = csr.M;
+    const Vcsr v = build_vcsr(csr, segw, bundle, layout, 2);
+    const TileView tv = make_tile_view(v, kTileMmaRows, 2, true);
+    orc_cst c{};
+    if (orc_build_cst(M, csr.N, csr.row_ptr.data(), csr.col.data(), csr.val.data(), &c) != 0)
+        return fail("oracle build_cst", M, 16);
+    int bad = 0;
+    const int W = c.num_windows, np = (int)tv.pieces.size() / 4;
+    const int64_t E = tv.n_entries();
+    if (tv.n_tiles != W) bad = fail("tile count differs from window count", M, 16);
+    // First entry of each window's tile: its first piece.
+    std::vector<int64_t> first(W + 1, -1);
+    first[W] = E;
+    for (int p = 0; p < np && !bad; ++p) {
+        const int w = tv.pieces[4 * p] / 16;
+        if (first[w] < 0) first[w] = tv.pieces[4 * p + 2];
+    }
+    int dup_windows = 0, empty_windows = 0;
+    for (int w = 0; w < W && !bad; ++w) {
+        const int r0 = 16 * w, nr = std::min(16, M - r0);
+        const int t0 = c.window_off[w], nt = c.window_off[w + 1] - t0;
+        const int64_t e0 = first[w], e1 = first[w + 1];
+        if (e0 < 0 || e1 < e0) { bad = fail("window's tile not found", M, 16); break; }
+        bool dup = false;
+        for (int r = r0; r < r0 + nr; ++r)
+            for (int p = csr.row_ptr[r] + 1; p < csr.row_ptr[r + 1]; ++p)
+                for (int q = csr.row_ptr[r]; q < p; ++q) dup |= csr.col[q] == csr.col[p];
+        if (nt == 0) {
+            ++empty_windows;
+            if (e1 - e0 != 16) { bad = fail("empty window not one placeholder group", M, 16); break; }
+            for (int64_t e = e0; e < e1; ++e)
+                if (tv.mask[e] != 0 || tv.brow[e] != 0) bad = fail("empty window holds a value", M, 16);
+            continue;
+        }
+        if (!dup) {
+            if (e1 - e0 != 16LL * nt) { bad = fail("entries differ from 16 per TCB", M, 16); break; }
+            for (int t = 0; t < nt && !bad; ++t) {
+                const int T = t0 + t;
+                for (int j = 0; j < 16; ++j) {
+                    const int64_t e = e0 + 16 * t + j;
+                    const int col = c.tcb2b[16 * T + j];
+                    if (col < 0 ? (tv.mask[e] != 0 || tv.brow[e] != 0)
+                                : (tv.mask[e] == 0 || tv.brow[e] != col))
+                        bad = fail("entry differs from tcb2B", M, 16);
+                }
+                for (int lr = 0; lr < 16 && !bad; ++lr) {
+                    // (local column, value) of the TCB row, against the view's.
+                    std::vector<std::pair<int, float>> a, b;
+                    for (int i = c.tcb_row_off[17 * T + lr]; i < c.tcb_row_off[17 * T + lr + 1]; ++i)
+                        a.emplace_back(c.col_idx[i], c.value[i]);
+                    for (int j = 0; j < 16; ++j) {
+                        const int64_t e = e0 + 16 * t + j;
+                        if ((tv.mask[e] >> lr) & 1)
+                            b.emplace_back(j, tv.val[(size_t)tile_val_index(16, e, lr)]);
+                    }
+                    std::sort(a.begin(), a.end(), [](auto& x, auto& y) { return x.first < y.first; });
+                    bool eq = a.size() == b.size() && (lr < nr || a.empty());
+                    for (size_t i = 0; eq && i < a.size(); ++i)
+                        eq = a[i].first == b[i].first && same_bits(a[i].second, b[i].second);
+                    if (!eq) bad = fail("TCB row differs from the view's", M, 16);
+                }
+            }
+            continue;
+        }
+        ++dup_windows;
+        std::vector<std::tuple<int, int, uint32_t>> a, b;
+        std::vector<int> cols, brows;
+        for (int t = t0; t < t0 + nt; ++t) {
+            for (int j = 0; j < 16; ++j)
+                if (c.tcb2b[16 * t + j] >= 0) cols.push_back(c.tcb2b[16 * t + j]);
+            for (int lr = 0; lr < 16; ++lr)
+                for (int i = c.tcb_row_off[17 * t + lr]; i < c.tcb_row_off[17 * t + lr + 1]; ++i) {
+                    uint32_t bits;
+                    std::memcpy(&bits, &c.value[i], 4);
+                    a.emplace_back(r0 + lr, c.tcb2b[16 * t + c.col_idx[i]], bits);
+                }
+        }
+        for (int64_t e = e0; e < e1; ++e) {
+            if (tv.mask[e] == 0) continue;
+            brows.push_back(tv.brow[e]);
+            for (int lr = 0; lr < nr; ++lr)
+                if ((tv.mask[e] >> lr) & 1) {
+                    uint32_t bits;
+                    const float x = tv.val[(size_t)tile_val_index(16, e, lr)];
+                    std::memcpy(&bits, &x, 4);
+                    b.emplace_back(r0 + lr, tv.brow[e], bits);
+                }
+        }
+        std::sort(a.begin(), a.end());
+        std::sort(b.begin(), b.end());
+        brows.erase(std::unique(brows.begin(), brows.end()), brows.end());
+        if (a != b) bad = fail("window nonzeros differ from the CST's", M, 16);
+        if (brows != cols) bad = fail("window columns differ from the CST's", M, 16);
+    }
+    if (!bad)
+        std::printf("cst ok M=%d nnz=%d windows=%d tcbs=%d empty=%d with-duplicates=%d entries=%lld\n",
+                    M, csr.nnz, W, c.num_tcb, empty_windows, dup_windows, (long long)E);
+    orc_free(c.window_off);
+    orc_free(c.tcb_col_off);
+    orc_free(c.tcb_row_off);
+    orc_free(c.col_idx);
+    orc_free(c.value);
+    orc_free(c.tcb2b);
+    return bad;
 }
 
 static int check(const Csr& csr, int segw, int bundle, int layout, int R_req, int expect_R,
@@ -191,6 +331,38 @@ int main() {
     bad |= check(block_matrix(9, 30, 3, 300, 7, 3, 75, true), 4, 64, kLayoutS, 16, 16, true);
     bad |= check(block_matrix(9, 30, 3, 300, 7, 3, 75, true), 4, 64, kLayoutH, 4, 4, true);
     bad |= check(block_matrix(37, 4, 16, 8192, 700, 4, 90, false), 4, 64, kLayoutS, 16, 16, true);
+    // The same windows against FastSpMM's condensed tiles: random rows
+    // (cfg1), 3-row blocks with duplicates, windows over 1024 columns (cut
+    // into pieces), and a partial last window after empty ones.
+    bad |= check_cst(cfg1, 4, 64, kLayoutS);
+    bad |= check_cst(block_matrix(9, 30, 3, 300, 7, 3, 75, true), 4, 64, kLayoutS);
+    bad |= check_cst(block_matrix(9, 30, 3, 300, 7, 3, 75, true), 8, 32, kLayoutH);
+    bad |= check_cst(block_matrix(38, 11, 16, 900, 9, 16, 100, false), 16, 16, kLayoutTC);
+    bad |= check_cst(block_matrix(37, 4, 16, 8192, 700, 4, 90, false), 4, 64, kLayoutS);
+    {
+        Coo e;
+        e.M = 16 * 5 + 7;
+        e.N = 64;
+        for (int r : {2, 3, 84, 86})
+            for (int k = 0; k < 20; ++k) {
+                e.rows.push_back(r);
+                e.cols.push_back((r * 7 + k * 3) % 64);
+                e.vals.push_back(0.25f * (float)(k - 9));
+            }
+        bad |= check_cst(coo_to_csr(e), 4, 64, kLayoutS);
+        // Windows of about 3,000 distinct columns and no repeated one (cut
+        // into pieces of up to 1024 entries).
+        Coo g;
+        g.M = 40;
+        g.N = 8192;
+        for (int r = 0; r < g.M; ++r)
+            for (int k = 0; k < 400; ++k) {
+                g.rows.push_back(r);
+                g.cols.push_back((r * 37 + k * 5) % g.N);
+                g.vals.push_back((float)((r + 3 * k) % 17 - 8) / 4.f);
+            }
+        bad |= check_cst(coo_to_csr(g), 4, 64, kLayoutS);
+    }
     // Tiles wider than one work item (split into pieces with partial sums).
     for (int R : {1, 3, 8}) bad |= check(block_matrix(20 + R, 6, 8, 4096, 300, 4, 90, false), 4, 64, kLayoutS, R, R);
     bad |= check(block_matrix(36, 4, 16, 8192, 700, 4, 90, false), 4, 64, kLayoutS, 16, 16);

@@ -304,3 +304,122 @@ def test_threaded_spmm_is_the_single_thread_result(orc, nthreads):
                               one32.view(np.uint32))
         assert np.array_equal(orc.spmm_f64(M, rp, col, val, B, nthreads).view(np.uint64),
                               one64.view(np.uint64))
+
+
+# ------------------------------------------------- FastSpMM condensed tiles
+def _cst_hand_csr():
+    """35 x 40: window 0 (rows 0-15) holds 17 distinct columns (two TCBs),
+    with an unsorted row and a row holding column 5 twice; window 1 (rows
+    16-31) is empty; window 2 (rows 32-34) is partial."""
+    rows = {0: [(20, 2.0), (3, 1.0)], 2: [(5, 4.0), (5, 0.5)],
+            7: [(21 + j, 10.0 + j) for j in range(14)], 33: [(39, -1.0), (0, 7.0)]}
+    row_ptr, col, val = [0], [], []
+    for r in range(35):
+        for c, v in rows.get(r, []):
+            col.append(c)
+            val.append(v)
+        row_ptr.append(len(col))
+    return (np.array(row_ptr, np.int32), np.array(col, np.int32), np.array(val, np.float32))
+
+
+def test_cst_hand_case(orc):
+    """src/fastspmm.cu:129-251 worked by hand on _cst_hand_csr: window 0's
+    columns [3, 5, 20, 21..34] fill TCB 0 (3, 5, 20, 21..33) and TCB 1 (34,
+    then padding); entries keep CSR order inside a row (row 0: 20 before 3;
+    both column-5 entries of row 2); window 1 adds no TCB; window 2 is TCB 2
+    with columns [0, 39]."""
+    rp, col, val = _cst_hand_csr()
+    s = orc.build_cst(35, 40, rp, col, val)
+    assert s["num_windows"] == 3 and s["num_tcb"] == 3
+    assert s["window_off"].tolist() == [0, 2, 2, 3]
+    assert s["tcb_col_off"].tolist() == [0, 17, 18, 20]
+    assert s["tcb_row_off"].tolist() == (
+        [0, 2, 2, 4, 4, 4, 4, 4, 17, 17, 17, 17, 17, 17, 17, 17, 17]
+        + [17] * 8 + [18] * 9
+        + [18, 18] + [20] * 15)
+    assert s["col_idx"].tolist() == [2, 0, 1, 1] + list(range(3, 16)) + [0] + [1, 0]
+    assert s["value"].tolist() == [2.0, 1.0, 4.0, 0.5] + [10.0 + j for j in range(13)] + [23.0] + [-1.0, 7.0]
+    assert s["tcb2b"].tolist() == ([3, 5, 20] + list(range(21, 34)) + [34] + [-1] * 15
+                                   + [0, 39] + [-1] * 14)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_cst_properties(orc, seed):
+    """What the layout must satisfy, computed independently with numpy:
+    each window's TCB columns are its sorted distinct columns padded with -1
+    to whole TCBs; the offsets chain (a TCB's first row offset is its first
+    entry, its 17th the next TCB's); and walking every TCB row puts every
+    nonzero of A back in its row and column exactly once, in CSR order."""
+    rng = np.random.default_rng(seed)
+    M, N = int(rng.integers(17, 120)), int(rng.integers(20, 300))
+    rp, col, val = csr_of(orc, M, N, *random_csr(rng, M, N, density=0.08, dup_rate=0.1,
+                                                 empty_rows=0.3))
+    # Rows in any column order (the layout keeps CSR order inside a row).
+    perm = np.concatenate([rp[r] + rng.permutation(rp[r + 1] - rp[r]) for r in range(M)])
+    col, val = col[perm.astype(np.int64)], val[perm.astype(np.int64)]
+    # Two empty windows in the middle.
+    if M > 48:
+        lo, hi = rp[16], rp[48]
+        col = np.concatenate([col[:lo], col[hi:]])
+        val = np.concatenate([val[:lo], val[hi:]])
+        rp = np.concatenate([rp[:17], np.full(32, lo), rp[49:] - (hi - lo)]).astype(np.int32)
+    s = orc.build_cst(M, N, rp, col, val)
+    W = (M + 15) // 16
+    assert s["num_windows"] == W and s["window_off"][0] == 0
+    ro, co, t2b = s["tcb_row_off"], s["tcb_col_off"], s["tcb2b"]
+    T = s["num_tcb"]
+    assert co[0] == 0 and co[-1] == len(s["col_idx"]) == rp[-1]
+    for t in range(T):
+        assert ro[17 * t] == co[t] and ro[17 * t + 16] == co[t + 1]
+        assert np.all(np.diff(ro[17 * t:17 * t + 17]) >= 0)
+    dense = np.zeros((M, N))
+    want = np.zeros((M, N))
+    for r in range(M):
+        np.add.at(want[r], col[rp[r]:rp[r + 1]], val[rp[r]:rp[r + 1]].astype(np.float64))
+    for w in range(W):
+        r0, r1 = 16 * w, min(M, 16 * w + 16)
+        cols = np.unique(col[rp[r0]:rp[r1]])
+        t0, t1 = s["window_off"][w], s["window_off"][w + 1]
+        assert t1 - t0 == (len(cols) + 15) // 16
+        padded = np.full(16 * (t1 - t0), -1)
+        padded[:len(cols)] = cols
+        assert np.array_equal(t2b[16 * t0:16 * t1], padded)
+        for lr in range(16):
+            got = []
+            for t in range(t0, t1):
+                for i in range(ro[17 * t + lr], ro[17 * t + lr + 1]):
+                    assert lr < r1 - r0
+                    c = t2b[16 * t + int(s["col_idx"][i])]
+                    assert c >= 0
+                    dense[r0 + lr, c] += s["value"][i]
+                    got.append((t, c, s["value"][i]))
+            if lr < r1 - r0:
+                # Per TCB, the row's entries in CSR order.
+                r = r0 + lr
+                row = list(zip(col[rp[r]:rp[r + 1]].tolist(), val[rp[r]:rp[r + 1]].tolist()))
+                for t in range(t0, t1):
+                    mine = set(t2b[16 * t:16 * t + 16].tolist())
+                    assert [(c, v) for (tt, c, v) in got if tt == t] == \
+                        [(c, v) for (c, v) in row if c in mine]
+    assert np.array_equal(dense, want)
+
+
+def test_cst_row_offsets_past_16_bits(orc):
+    """The reference stores the absolute row offsets as uint16_t
+    (fastspmm.cu:216,225) and its kernel subtracts the TCB's 32-bit first
+    entry (fastspmm.cu:61-71): once a matrix passes 65535 entries, the
+    16-bit offsets no longer give a TCB row's extent.  The restatement keeps
+    int offsets, so every TCB row still indexes its own entries."""
+    M, N = 64, 4096
+    rng = np.random.default_rng(5)
+    rp = np.arange(0, M * 1200 + 1, 1200, dtype=np.int32)
+    col = np.concatenate([np.sort(rng.choice(N, 1200, replace=False)) for _ in range(M)]).astype(np.int32)
+    val = np.ones(len(col), np.float32)
+    s = orc.build_cst(M, N, rp, col, val)
+    ro, co = s["tcb_row_off"].astype(np.int64), s["tcb_col_off"].astype(np.int64)
+    assert co[-1] == M * 1200 > 65535
+    base = np.repeat(co[:-1], 17)
+    start = ro - base
+    assert np.all((start >= 0) & (start <= np.repeat(np.diff(co), 17)))
+    wrapped = (ro & 0xFFFF) - base
+    assert np.any(wrapped < 0)
