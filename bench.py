@@ -136,6 +136,47 @@ def copy_rate_gbs(vs, st, nbytes=512 << 20, reps=10):
     return 2.0 * nbytes / (ms * 1e-3) / 1e9
 
 
+def slice_path_report(w, li, kernel_ms):
+    """The rate at which the tile kernel moves its B-row slices (view
+    entries x O x 4 bytes per SpMM) from the caches to the CUs, set against
+    the probe (lib/libvcsr_probe.so) reading slices of the same width and
+    per-lane vector at random from a 2 MiB buffer (L2-resident: the
+    practical ceiling of that path) and from a buffer the size of B (served
+    by the MALL or HBM).  None where the timed kernel is not the vector-ALU
+    tile kernel or its slices are not a power-of-two number of lanes."""
+    import ctypes as C
+    if li["matrix_cores"] or li["entries"] <= 0 or li["vec"] not in (1, 2, 4):
+        return None
+    slice_floats = li["slice_cols"]
+    lps = slice_floats // li["vec"]
+    if slice_floats % li["vec"] or not 1 <= lps <= 64 or lps & (lps - 1):
+        return None
+    lib = C.CDLL(os.path.join(ROOT, "vcsr-spmm_amd", "lib", "libvcsr_probe.so"))
+    fn = lib.vcsr_probe_slice_reads
+    fn.argtypes = [C.c_uint64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_double),
+                   C.POINTER(C.c_double)]
+    fn.restype = C.c_int
+
+    def probe(nbytes):
+        rate, ms = C.c_double(), C.c_double()
+        rc = fn(nbytes, slice_floats, li["vec"], 10, C.byref(rate), C.byref(ms))
+        if rc != 0:
+            raise RuntimeError(f"slice probe failed ({rc})")
+        return rate.value / 1e12
+
+    b_bytes = w.csr.N * slice_floats * 4
+    l2 = probe(2 << 20)
+    bsz = probe(max(b_bytes, 2 << 20))
+    kern = li["entries"] * w.O * 4 / (kernel_ms * 1e-3) / 1e12
+    return {"slice_bytes": slice_floats * 4, "vec_floats": li["vec"],
+            "kernel_tb_s": round(kern, 2), "probe_l2_resident_tb_s": round(l2, 2),
+            "probe_b_sized_tb_s": round(bsz, 2), "frac_of_l2_resident": round(kern / l2, 4),
+            "what": "B-row slices moved from the caches to the CUs per second: the timed "
+                    "kernel (view entries x O x 4 bytes / kernel time) against a probe "
+                    "reading random slices of the same shape from a 2 MiB buffer "
+                    "(L2-resident) and from one of B's size (N x slice x 4 bytes)"}
+
+
 def host_threads():
     """Threads the CPU baseline may use: the cores this process may run on,
     at most 16 (one GPU's share of the GPU box's host) and at most
@@ -536,6 +577,11 @@ def main():
         copy = copy_rate_gbs(vs, st)
         out["roofline"]["copy_gbs"] = round(copy, 1)
         out["roofline"]["frac_of_copy"] = round(achieved / copy, 4)
+        if fmt is not None and args.algo in ("vcsr", "tile", "fast"):
+            # The path that binds the tile kernel: B-row slices from the caches.
+            sp = slice_path_report(w, fmt.launch_info(O, vs.KERNEL_TILE), kernel_ms)
+            if sp is not None:
+                out["roofline"]["b_slice_path"] = sp
     checks = [check]
     if (not args.no_extras and args.config == "cfg2" and args.algo == "vcsr"
             and args.cols is None):

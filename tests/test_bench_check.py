@@ -46,6 +46,28 @@ def test_cpu_baseline_threads(bench):
     assert set(d) == {"cpu_model", "nproc", "affinity_cpus"}
 
 
+def test_slice_probe_library_rejects_bad_shapes():
+    """bench.py's slice-read probe (lib/libvcsr_probe.so, built beside the
+    library) loads and refuses, before any GPU call, the shapes its kernel
+    cannot read in bounds: a vector width other than 1, 2 or 4 floats, a
+    slice that is not a power-of-two number of lanes up to 64, a buffer
+    smaller than one slice, and no output pointers."""
+    import ctypes as C
+    path = os.path.join(ROOT, "vcsr-spmm_amd", "lib", "libvcsr_probe.so")
+    if not os.path.exists(path):
+        pytest.skip("probe library not built (run __graft_entry__.build())")
+    fn = C.CDLL(path).vcsr_probe_slice_reads
+    fn.argtypes = [C.c_uint64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_double),
+                   C.POINTER(C.c_double)]
+    fn.restype = C.c_int
+    r, m = C.c_double(), C.c_double()
+    for nbytes, floats, vec, reps in [(1 << 20, 128, 3, 5), (1 << 20, 96, 4, 5),
+                                      (1 << 20, 512, 4, 5), (1 << 20, 2, 4, 5),
+                                      (256, 128, 4, 5), (1 << 20, 128, 4, 0)]:
+        assert fn(nbytes, floats, vec, reps, C.byref(r), C.byref(m)) == 1, (nbytes, floats, vec)
+    assert fn(1 << 20, 128, 4, 5, None, None) == 1
+
+
 @pytest.mark.gpu
 def test_bench_line_contract():
     """On the GPU: bench.py's one JSON line (short run) carries what the
@@ -75,6 +97,12 @@ def test_bench_line_contract():
     assert roof["traffic"] and roof["traffic"] > 0
     assert roof["traffic_source"]["commit"] and "kernel_sources_match" in roof["traffic_source"]
     assert roof["copy_gbs"] > 0 and 0 < roof["frac_of_copy"] < 1.5
+    # The B-row slice path that binds the tile kernel, against the probe.
+    sp = roof["b_slice_path"]
+    assert sp["slice_bytes"] == 512 and sp["vec_floats"] == 4
+    assert sp["probe_l2_resident_tb_s"] > 0 and sp["probe_b_sized_tb_s"] > 0
+    assert 0 < sp["frac_of_l2_resident"] < 1.2
+    assert abs(sp["frac_of_l2_resident"] - sp["kernel_tb_s"] / sp["probe_l2_resident_tb_s"]) < 0.02
     cpu = d["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["value"] > 0 and cpu["cores"] >= 1
     assert cpu["single_thread"]["cores"] == 1 and cpu["host"]

@@ -139,6 +139,13 @@ struct TileShape {
     // per stream and at most one each of U/2, U/4, ... UT (UT = 2).
     static constexpr int UT = U >= 2 ? 2 : U;
     static constexpr int EPAD = (EMAX + S * U - 1) / (S * U) * (S * U);
+    // Single-row tiles with several work items per wave: each stream takes
+    // an equal run of the wave's entries, cutting pieces where the runs
+    // meet (the piece's owner adds the other streams' partial sums after the
+    // loop).  Whole pieces per stream leave most streams idle behind a long
+    // row's piece: power-law 322K matrix, O = 8, 41% of the B-load slots
+    // busy against 84%.
+    static constexpr bool EQ = R == 1 && MERGE > 1;
 };
 
 // One wave's LDS: staged entries (B-row byte offsets and values), the piece
@@ -148,6 +155,10 @@ template <int VEC, int LPE, int R, int MERGE>
 struct TileLds {
     using Sh = TileShape<VEC, LPE, R, MERGE>;
     __align__(16) float val[Sh::EPAD * Sh::RS];
+    // Equal-run streams: per lane, the partial sum of the piece open at its
+    // stream's first entry, and per stream that piece (-1: none).
+    typename VecT<VEC>::T xs[Sh::EQ ? 64 * R : 1];
+    int32_t headp[Sh::EQ ? Sh::S : 1];
     uint32_t brow[Sh::EPAD];
     int4 piece[Sh::PMAX + 2];
     int32_t first[Sh::S + 1];
@@ -304,21 +315,42 @@ __device__ __forceinline__ void tile_item(
     };
 
     if (np > 1) {
-        // Stream s takes the pieces whose entry midpoint falls in the s-th
-        // S-quantile of the item: first piece lf[s], end piece lf[s + 1].
-        if (lane <= S) {
-            int32_t lo = 0, hi = np;
+        int32_t pa, pb, tb, te;  // this stream's pieces and entries
+        if constexpr (Sh::EQ) {
+            // Entries tb .. te-1, and pa the piece holding entry tb (the
+            // last piece starting at or before it; pieces are not empty).
+            tb = (sub * ne) / S;
+            te = ((sub + 1) * ne) / S;
+            int32_t lo = 0, hi = np - 1;
             while (lo < hi) {
-                const int32_t mid = (lo + hi) >> 1;
-                const int32_t sm = ((lp[mid].z + lp[mid + 1].z) * S) / (2 * ne);
-                if (sm < lane) lo = mid + 1;
-                else hi = mid;
+                const int32_t mid = (lo + hi + 1) >> 1;
+                if (lp[mid].z <= tb) lo = mid;
+                else hi = mid - 1;
             }
-            lf[lane] = lo;
+            pa = lo;
+            pb = pa;  // set after the loop: the first piece not completed
+        } else {
+            // Stream s takes the pieces whose entry midpoint falls in the s-th
+            // S-quantile of the item: first piece lf[s], end piece lf[s + 1].
+            if (lane <= S) {
+                int32_t lo = 0, hi = np;
+                while (lo < hi) {
+                    const int32_t mid = (lo + hi) >> 1;
+                    const int32_t sm = ((lp[mid].z + lp[mid + 1].z) * S) / (2 * ne);
+                    if (sm < lane) lo = mid + 1;
+                    else hi = mid;
+                }
+                lf[lane] = lo;
+            }
+            wave_sync();
+            pa = lf[sub];
+            pb = lf[sub + 1];
+            tb = lp[pa].z;
+            te = lp[pb].z;
         }
-        wave_sync();
-        const int32_t pa = lf[sub], pb = lf[sub + 1];
-        const int32_t tb = lp[pa].z, te = lp[pb].z;  // this stream's entries
+        // Equal runs: piece pa began in an earlier stream's run; this stream
+        // only contributes a partial sum to it.
+        const bool carry = Sh::EQ && lp[pa].z < tb;
         // Lanes of this lane's stream, for ballots.
         const uint64_t smask =
             LPE == 64 ? ~0ull : (((1ull << (LPE & 63)) - 1ull) << ((sub * LPE) & 63));
@@ -334,9 +366,9 @@ __device__ __forceinline__ void tile_item(
             const int32_t k = k0 + kl * VEC;
             const bool kok = k < O;
             const uint32_t koff = (uint32_t)((kok || BUF) ? k : 0) * 4u;
-            V acc[R];
+            V acc[R], hacc[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
+            for (int r = 0; r < R; ++r) acc[r] = hacc[r] = zero_vec(V());
             int32_t p = pa, pend = lp[pa + 1].z;
             bool bad = false;
             auto block = [&](auto full_c, int32_t i0) {
@@ -354,15 +386,22 @@ __device__ __forceinline__ void tile_item(
                     const bool ok = FULL || t < te;
                     apply(acc, ok ? t : 0, ok, b[u]);
                     if (ok && t + 1 == pend) {
-                        // A stream stores a piece only if all its lanes' sums
-                        // are finite; otherwise redo_piece computes and stores
-                        // it after the loop.
-                        const uint64_t bm = __ballot(!piece_finite(acc, kok));
-                        if ((bm & smask) != 0) {
-                            bad = true;
-                            lbad[p] = 1;
+                        if (carry && p == pa) {
+                            // The end of a piece begun in an earlier run: its
+                            // owner adds this partial sum after the loop.
+#pragma unroll
+                            for (int r = 0; r < R; ++r) hacc[r] = acc[r];
                         } else {
-                            store_piece(lp[p], acc, k, kok);
+                            // A stream stores a piece only if all its lanes'
+                            // sums are finite; otherwise redo_piece computes
+                            // and stores it after the loop.
+                            const uint64_t bm = __ballot(!piece_finite(acc, kok));
+                            if ((bm & smask) != 0) {
+                                bad = true;
+                                lbad[p] = 1;
+                            } else {
+                                store_piece(lp[p], acc, k, kok);
+                            }
                         }
 #pragma unroll
                         for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
@@ -374,6 +413,33 @@ __device__ __forceinline__ void tile_item(
             for (int32_t i0 = 0; i0 < nmax; i0 += U) {
                 if (i0 + U <= nmin) block(std::true_type(), i0);
                 else block(std::false_type(), i0);
+            }
+            if constexpr (Sh::EQ) {
+                // Piece p is still open at the end of the run when it began
+                // before te.  If it is piece pa begun in an earlier run, the
+                // whole run was a middle part of it; otherwise this stream
+                // owns it and adds the following runs' partial sums (each
+                // stream's first piece and its sum up to that piece's end or
+                // its run's) in stream order.
+                pb = p;
+                const bool open = lp[p].z < te || (te == tb && carry);
+                const bool middle = open && carry && p == pa;
+                if (carry) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) L.xs[lane * R + r] = middle ? acc[r] : hacc[r];
+                }
+                if (kl == 0) L.headp[sub] = carry ? pa : -1;
+                wave_sync();
+                if (open && !middle) {
+                    for (int32_t s2 = sub + 1; s2 < S && L.headp[s2] == p; ++s2)
+#pragma unroll
+                        for (int r = 0; r < R; ++r)
+                            acc[r] = add_vec(acc[r], L.xs[(s2 * LPE + kl) * R + r]);
+                    const uint64_t bm = __ballot(!piece_finite(acc, kok));
+                    if ((bm & smask) != 0) redo_piece(lp[p], lp[p].z, lp[p + 1].z, k, koff, kok);
+                    else store_piece(lp[p], acc, k, kok);
+                }
+                wave_sync();
             }
             if (__any(bad)) {
                 wave_sync();
