@@ -143,8 +143,11 @@ struct TileShape {
     // an equal run of the wave's entries, cutting pieces where the runs
     // meet (the piece's owner adds the other streams' partial sums after the
     // loop).  Whole pieces per stream leave most streams idle behind a long
-    // row's piece: power-law 322K matrix, O = 8, 41% of the B-load slots
-    // busy against 84%.
+    // row's piece: power-law 322K matrix, O = 8 / 32, 41% of the B-load
+    // slots busy against 84%, 37.1 / 46.1 against 30.0 / 40.1 us.  A stream
+    // that ends a piece begun in an earlier run writes its partial sum to
+    // LDS at once (held in registers, the 16-byte-vector build kept it on
+    // the stack and ran 1.7x slower).
     static constexpr bool EQ = R == 1 && MERGE > 1;
 };
 
@@ -366,9 +369,9 @@ __device__ __forceinline__ void tile_item(
             const int32_t k = k0 + kl * VEC;
             const bool kok = k < O;
             const uint32_t koff = (uint32_t)((kok || BUF) ? k : 0) * 4u;
-            V acc[R], hacc[R];
+            V acc[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = hacc[r] = zero_vec(V());
+            for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
             int32_t p = pa, pend = lp[pa + 1].z;
             bool bad = false;
             auto block = [&](auto full_c, int32_t i0) {
@@ -390,7 +393,7 @@ __device__ __forceinline__ void tile_item(
                             // The end of a piece begun in an earlier run: its
                             // owner adds this partial sum after the loop.
 #pragma unroll
-                            for (int r = 0; r < R; ++r) hacc[r] = acc[r];
+                            for (int r = 0; r < R; ++r) L.xs[lane * R + r] = acc[r];
                         } else {
                             // A stream stores a piece only if all its lanes'
                             // sums are finite; otherwise redo_piece computes
@@ -424,9 +427,9 @@ __device__ __forceinline__ void tile_item(
                 pb = p;
                 const bool open = lp[p].z < te || (te == tb && carry);
                 const bool middle = open && carry && p == pa;
-                if (carry) {
+                if (middle) {
 #pragma unroll
-                    for (int r = 0; r < R; ++r) L.xs[lane * R + r] = middle ? acc[r] : hacc[r];
+                    for (int r = 0; r < R; ++r) L.xs[lane * R + r] = acc[r];
                 }
                 if (kl == 0) L.headp[sub] = carry ? pa : -1;
                 wave_sync();
