@@ -95,8 +95,9 @@ def assert_within_tolerance(C, ref64, row_ptr, val, B, what=""):
 
 
 def random_csr(rng, M, N, density=0.05, dup_rate=0.0, empty_rows=0.0, max_row=None):
-    """Random CSR arrays (row_ptr, col, val) as the reference would build
-    them from an unsorted COO: columns sorted per row, duplicates allowed."""
+    """Random COO arrays (rows, cols, vals), rows ascending and each row's
+    columns shuffled, duplicates allowed: the unsorted input the reference's
+    COO -> CSR conversion takes."""
     rows, cols = [], []
     for r in range(M):
         if rng.random() < empty_rows:

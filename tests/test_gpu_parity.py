@@ -394,6 +394,81 @@ def test_nonfinite_b_stays_in_its_columns(gpu, orc, st, kind, tile_rows, O):
     assert np.allclose(C[fin], ref[fin], rtol=1e-5, atol=1e-4)
 
 
+def _row_lengths_csr(vs, rng, lengths, N):
+    """One row per entry of `lengths`, that many distinct random columns."""
+    rows, cols = [], []
+    for r, k in enumerate(lengths):
+        c = rng.choice(N, size=k, replace=False) if k else np.zeros(0, np.int64)
+        rows.extend([r] * k)
+        cols.extend(c.tolist())
+    vals = rng.uniform(-1, 1, size=len(rows)).astype(np.float32)
+    return vs.coo_to_csr(vs.Coo.from_arrays(len(lengths), N, np.array(rows, np.int32),
+                                            np.array(cols, np.int32), vals))
+
+
+# Row lengths that mix short rows (merged into shared work items), rows of
+# 17-64 entries (one piece, a work item of their own), rows cut into pieces
+# of up to 64 entries (partial rows summed by the reduce kernel) and empty
+# rows, so that a wave's four work items hold pieces of every length.
+_EQ_PATTERN = [0, 1, 3, 17, 2, 150, 5, 64, 65, 9, 400, 1, 1, 30, 0, 12, 2, 2, 90, 7]
+
+
+@pytest.mark.parametrize("O", [1, 4, 8, 32])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_equal_runs_of_single_row_tiles(gpu, orc, st, O, accumulate):
+    """Single-row tiles at O <= 8 and O = 32 run four work items per wave,
+    each of 8 streams taking an equal run of the wave's entries; a piece cut
+    between runs is finished by the stream that began it from the later
+    streams' partial sums.  Rows of every length, pieces spanning up to
+    seven runs, and a matrix with fewer entries than streams (empty runs):
+    all of C within the north-star bounds, in both C modes, the same bits
+    on a second call."""
+    vs = gpu
+    rng = np.random.default_rng(500 + O)
+    cases = [_row_lengths_csr(vs, rng, _EQ_PATTERN * 12, 1000),
+             _row_lengths_csr(vs, rng, [1, 0, 2, 0, 1], 9)]
+    for csr in cases:
+        print(f"equal runs M={csr.M} nnz={csr.nnz} O={O} accumulate={accumulate}", flush=True)
+        fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+        fmt.set_tile_rows(1)
+        fmt.upload(st)
+        li = fmt.launch_info(O, vs.KERNEL_TILE)
+        assert li["tile_rows"] == 1 and (li["vec"] == 4 if O == 32 else li["vec"] == 1)
+        B = vs.gen_dense(O + 3, 0, csr.N, O)
+        C0 = rng.uniform(-2, 2, size=(csr.M, O)).astype(np.float32)
+        ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+        got = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate)
+        again = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate)
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+        assert_within_tolerance(got - C0 if accumulate else got, ref64, csr.row_ptr, csr.val, B,
+                                f"equal runs O={O}")
+
+
+@pytest.mark.parametrize("O", [8, 32])
+def test_equal_runs_nonfinite_b(gpu, orc, st, O):
+    """Inf and NaN in B rows read by long rows (pieces cut between streams'
+    runs, and split rows) and by short ones reach exactly the C entries the
+    reference's loop reaches: the stream that finishes a piece from other
+    streams' partial sums recomputes it with the presence bits when the sum
+    is not finite."""
+    vs = gpu
+    rng = np.random.default_rng(900 + O)
+    csr = _row_lengths_csr(vs, rng, _EQ_PATTERN * 6, 600)
+    B = vs.gen_dense(O, 0, csr.N, O)
+    rp, col = csr.row_ptr, csr.col
+    long_row = int(np.argmax(np.diff(rp)))
+    B[col[rp[long_row] + 3], 0] = np.inf
+    B[col[rp[long_row + 13]], :] = np.nan                # a row in another work item
+    B[col[rp[3 * len(_EQ_PATTERN) + 8] + 40], O - 1] = -np.inf  # a 65-entry row's second piece
+    ref = orc.spmm_f32(csr.M, rp, col, csr.val, B)
+    C = _run(vs, "tile", csr, B, st, tile_rows=1)
+    assert np.array_equal(np.isnan(C), np.isnan(ref))
+    assert np.array_equal(np.isposinf(C), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(C), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    assert np.allclose(C[fin], ref[fin], rtol=1e-5, atol=1e-4)
+
+
 @pytest.mark.parametrize("kind,tile_rows", [("row", 0), ("tile", 0), ("tile", 16)])
 def test_b_of_2gb_or_more_uses_64bit_addresses(gpu, orc, st, kind, tile_rows):
     """B of 2^31 bytes or more cannot be addressed with 32-bit buffer
