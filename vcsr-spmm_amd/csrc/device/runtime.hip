@@ -259,6 +259,9 @@ int vcsr_fmt_upload(vcsr_fmt* fmt, void* stream) {
             d.tv_n_entries = tv.n_entries();
             d.tv_split = upload_array(tv.split, st, "upload split tiles");
             d.tv_n_split = (int32_t)(tv.split.size() / 4);
+            d.tv_split_pieces.resize((size_t)d.tv_n_split);
+            for (int32_t i = 0; i < d.tv_n_split; ++i)
+                d.tv_split_pieces[(size_t)i] = tv.split[4 * (size_t)i + 3];
             d.tv_partial_rows = tv.n_partial_rows;
             // Partial rows of split tiles (tile kernel) and split rows (row
             // kernel): both are launched in column slices of at most 256

@@ -573,64 +573,89 @@ void vcsr_tile_kernel(
                                        ent_val, B, C, partials);
 }
 
-// Adds the piece partials of one row of a split tile into C; one block per
-// row.  split: {row, first partial row, stride, pieces}.  The block's 256
-// threads are `groups` groups of `cl` lanes: lane c of group g sums column
-// vector c of partials g, g + groups, ... (eight loads in flight for
-// 16-byte vectors, four otherwise: cfg3 O = 128 1% faster with eight, O = 8
-// 1% slower), and the groups are then added in LDS, so a row split into many
-// pieces costs a few load latencies instead of one per piece.
+// Adds the piece partials of the rows of split tiles into C.  split: {row,
+// first partial row, stride, pieces}, in decreasing piece count.  Lanes
+// work in groups of cl lanes (the smallest power of two covering the row's
+// column vectors, at most 64): lane c of group g sums column vector c of
+// partials g, g + groups, ... .
+//  - The first n_heavy rows (the most pieces) take a block of 256 threads
+//    each (eight loads in flight for 16-byte vectors, four otherwise: cfg3
+//    O = 128 1% faster with eight, O = 8 1% slower), whose groups are added
+//    in LDS, so a row split into many pieces costs a few load latencies
+//    instead of one per piece.
+//  - The other rows take one wave each, four per block, whose groups are
+//    added with lane shuffles: no LDS and no block barrier.  Most split rows
+//    have a few pieces (power-law 322K matrix: 2,740 rows, most with 2 to 8);
+//    as a block each they left most of the block idle behind its barriers.
+// Each row's sum has a fixed order (the same bits on every call).
 template <int VEC>
 __global__ __launch_bounds__(256) void vcsr_tile_reduce(int32_t O, int32_t ld, int32_t accumulate,
+                                                        int32_t n_heavy, int32_t n_split,
                                                         const int4* __restrict__ split,
                                                         const float* __restrict__ partials,
                                                         float* __restrict__ C) {
     using V = typename VecT<VEC>::T;
     __shared__ V red[256];
-    const int4 s = split[blockIdx.x];
     const int32_t nvec = (O + VEC - 1) / VEC;
     int32_t cl = 1;
     while (cl < nvec && cl < 64) cl <<= 1;
-    const int32_t groups = 256 / cl;
-    const int32_t tid = (int32_t)threadIdx.x, c = tid % cl, g = tid / cl;
-    const int64_t step = (int64_t)s.z * O;
-    auto part = [&](int32_t j, int32_t cv) {
-        return *reinterpret_cast<const V*>(partials + (int64_t)s.y * O + (int64_t)j * step +
-                                           (int64_t)cv * VEC);
+    auto part = [&](const int4& s, int32_t j, int32_t cv) {
+        return *reinterpret_cast<const V*>(partials + (int64_t)s.y * O +
+                                           (int64_t)j * ((int64_t)s.z * O) + (int64_t)cv * VEC);
     };
-    for (int32_t c0 = 0; c0 < nvec; c0 += cl) {
-        const int32_t cv = c0 + c;
-        V acc = zero_vec(V());
-        if (cv < nvec) {
-            int32_t j = g;
-            if constexpr (VEC == 4) {
-                for (; j + 7 * groups < s.w; j += 8 * groups) {
-                    const V x0 = part(j, cv), x1 = part(j + groups, cv);
-                    const V x2 = part(j + 2 * groups, cv), x3 = part(j + 3 * groups, cv);
-                    const V x4 = part(j + 4 * groups, cv), x5 = part(j + 5 * groups, cv);
-                    const V x6 = part(j + 6 * groups, cv), x7 = part(j + 7 * groups, cv);
-                    acc = add_vec(acc, add_vec(add_vec(add_vec(x0, x1), add_vec(x2, x3)),
-                                               add_vec(add_vec(x4, x5), add_vec(x6, x7))));
-                }
+    // acc += partials g, g + groups, ... of column vector cv of row s.
+    auto sum_group = [&](const int4& s, int32_t g, int32_t groups, int32_t cv, V acc) {
+        int32_t j = g;
+        if constexpr (VEC == 4) {
+            for (; j + 7 * groups < s.w; j += 8 * groups) {
+                const V x0 = part(s, j, cv), x1 = part(s, j + groups, cv);
+                const V x2 = part(s, j + 2 * groups, cv), x3 = part(s, j + 3 * groups, cv);
+                const V x4 = part(s, j + 4 * groups, cv), x5 = part(s, j + 5 * groups, cv);
+                const V x6 = part(s, j + 6 * groups, cv), x7 = part(s, j + 7 * groups, cv);
+                acc = add_vec(acc, add_vec(add_vec(add_vec(x0, x1), add_vec(x2, x3)),
+                                           add_vec(add_vec(x4, x5), add_vec(x6, x7))));
             }
-            for (; j + 3 * groups < s.w; j += 4 * groups) {
-                const V x0 = part(j, cv), x1 = part(j + groups, cv);
-                const V x2 = part(j + 2 * groups, cv), x3 = part(j + 3 * groups, cv);
-                acc = add_vec(acc, add_vec(add_vec(x0, x1), add_vec(x2, x3)));
-            }
-            for (; j < s.w; j += groups) acc = add_vec(acc, part(j, cv));
         }
-        red[tid] = acc;
-        __syncthreads();
-        for (int32_t h = groups / 2; h >= 1; h >>= 1) {
-            if (g < h) red[tid] = add_vec(red[tid], red[tid + h * cl]);
+        for (; j + 3 * groups < s.w; j += 4 * groups) {
+            const V x0 = part(s, j, cv), x1 = part(s, j + groups, cv);
+            const V x2 = part(s, j + 2 * groups, cv), x3 = part(s, j + 3 * groups, cv);
+            acc = add_vec(acc, add_vec(add_vec(x0, x1), add_vec(x2, x3)));
+        }
+        for (; j < s.w; j += groups) acc = add_vec(acc, part(s, j, cv));
+        return acc;
+    };
+    auto store = [&](const int4& s, int32_t cv, const V& x) {
+        V* dst = reinterpret_cast<V*>(C + (int64_t)s.x * ld + (int64_t)cv * VEC);
+        *dst = accumulate ? add_vec(*dst, x) : x;
+    };
+    if ((int32_t)blockIdx.x < n_heavy) {
+        const int4 s = split[blockIdx.x];
+        const int32_t groups = 256 / cl;
+        const int32_t tid = (int32_t)threadIdx.x, c = tid % cl, g = tid / cl;
+        for (int32_t c0 = 0; c0 < nvec; c0 += cl) {
+            const int32_t cv = c0 + c;
+            red[tid] = cv < nvec ? sum_group(s, g, groups, cv, zero_vec(V())) : zero_vec(V());
+            __syncthreads();
+            for (int32_t h = groups / 2; h >= 1; h >>= 1) {
+                if (g < h) red[tid] = add_vec(red[tid], red[tid + h * cl]);
+                __syncthreads();
+            }
+            if (g == 0 && cv < nvec) store(s, cv, red[tid]);
             __syncthreads();
         }
-        if (g == 0 && cv < nvec) {
-            V* dst = reinterpret_cast<V*>(C + (int64_t)s.x * ld + (int64_t)cv * VEC);
-            *dst = accumulate ? add_vec(*dst, red[tid]) : red[tid];
-        }
-        __syncthreads();
+        return;
+    }
+    // Light rows: wave w of block b takes row n_heavy + 4 (b - n_heavy) + w.
+    const int32_t i = n_heavy + ((int32_t)blockIdx.x - n_heavy) * 4 + (int32_t)(threadIdx.x >> 6);
+    if (i >= n_split) return;
+    const int4 s = split[i];
+    const int32_t lane = (int32_t)(threadIdx.x & 63u), groups = 64 / cl;
+    const int32_t c = lane % cl, g = lane / cl;
+    for (int32_t c0 = 0; c0 < nvec; c0 += cl) {
+        const int32_t cv = c0 + c;
+        V acc = cv < nvec ? sum_group(s, g, groups, cv, zero_vec(V())) : zero_vec(V());
+        for (int32_t h = cl; h < 64; h <<= 1) acc = add_vec(acc, shfl_xor_vec(acc, h));
+        if (g == 0 && cv < nvec) store(s, cv, acc);
     }
 }
 
@@ -928,9 +953,23 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
         if (e != hipSuccess) return e;
     }
     if (d.tv_n_split > 0) {
-        hipLaunchKernelGGL(vcsr_tile_reduce<VEC>, dim3((unsigned)d.tv_n_split), dim3(256), 0, st,
-                           O, ld, accumulate, reinterpret_cast<const int4*>(d.tv_split), partials,
-                           C);
+        // Rows whose pieces would take one wave more than four loads per
+        // lane get a block each (the split rows come in decreasing piece
+        // count, so they are the first n_heavy).  Power-law 322K matrix:
+        // O = 8 29.8 -> 28.6 us per SpMM (eight loads per lane: 29.1-29.4),
+        // O = 128 within the run-to-run range.
+        const int32_t nvec = (O + VEC - 1) / VEC;
+        int32_t cl = 1;
+        while (cl < nvec && cl < 64) cl <<= 1;
+        const int32_t light_max = 4 * (64 / cl);
+        const auto& pc = d.tv_split_pieces;
+        const int32_t n_heavy = (int32_t)(std::partition_point(pc.begin(), pc.end(),
+                                                               [&](int32_t x) { return x > light_max; }) -
+                                          pc.begin());
+        const int64_t blocks = (int64_t)n_heavy + ((int64_t)d.tv_n_split - n_heavy + 3) / 4;
+        hipLaunchKernelGGL(vcsr_tile_reduce<VEC>, dim3((unsigned)blocks), dim3(256), 0, st, O, ld,
+                           accumulate, n_heavy, d.tv_n_split,
+                           reinterpret_cast<const int4*>(d.tv_split), partials, C);
         return hipGetLastError();
     }
     return hipSuccess;

@@ -6,6 +6,7 @@
 
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "host/core.hpp"
 
@@ -49,6 +50,8 @@ struct DeviceFmt {
     int64_t tv_n_entries = 0;
     int32_t* tv_split = nullptr;        // 4*tv_n_split: row, partial row, stride, pieces
     int32_t tv_n_split = 0;
+    std::vector<int32_t> tv_split_pieces;  // host copy of the pieces per split row
+                                           // (in the split order: decreasing)
     int32_t tv_partial_rows = 0;
     // Partial sums of split rows / tiles (partials_floats floats): sized at
     // upload for every O (split rows and tiles are launched in column slices
