@@ -953,15 +953,18 @@ hipError_t launch_vec(const Vcsr& v, const DeviceFmt& d, const float* B, int32_t
         if (e != hipSuccess) return e;
     }
     if (d.tv_n_split > 0) {
-        // Rows whose pieces would take one wave more than four loads per
-        // lane get a block each (the split rows come in decreasing piece
-        // count, so they are the first n_heavy).  Power-law 322K matrix:
-        // O = 8 29.8 -> 28.6 us per SpMM (eight loads per lane: 29.1-29.4),
-        // O = 128 within the run-to-run range.
+        // Narrow B (at most 8 column vectors per row): rows whose pieces
+        // would take one wave more than four loads per lane get a block
+        // each (the split rows come in decreasing piece count, so they are
+        // the first n_heavy), the rest a wave each.  Power-law 322K matrix,
+        // O = 8: 29.8 -> 28.6 us per SpMM (eight loads per lane: 29.1-29.4;
+        // the kernel's own duration is the same, the gain is the launch of
+        // 0.7K blocks instead of 2.7K).  Wider B keeps a block per row: at
+        // O = 128 the reduce's duration was 5.9 against 5.3 us.
         const int32_t nvec = (O + VEC - 1) / VEC;
         int32_t cl = 1;
         while (cl < nvec && cl < 64) cl <<= 1;
-        const int32_t light_max = 4 * (64 / cl);
+        const int32_t light_max = cl <= 8 ? 4 * (64 / cl) : 0;
         const auto& pc = d.tv_split_pieces;
         const int32_t n_heavy = (int32_t)(std::partition_point(pc.begin(), pc.end(),
                                                                [&](int32_t x) { return x > light_max; }) -
