@@ -202,8 +202,10 @@ def test_cli_all_algorithms_full_size(vs, cfg):
 
 
 def test_integration_shim_compiles(tmp_path):
-    """The C++ shim INTEGRATION.md gives a maintainer of the reference
-    compiles against include/vcsr_spmm.h, with the reference's CSR struct
+    """The C++ shim that the repository's integration guide gives a
+    maintainer of the reference (its "C++ shim" section, read from the
+    guide at the repository root) compiles against include/vcsr_spmm.h,
+    with the reference's CSR struct
     (include/csr.hpp:8-13: M, N, nnz, row_ptr, col, val) and an opaque
     hipStream_t, as in the reference's translation unit."""
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
