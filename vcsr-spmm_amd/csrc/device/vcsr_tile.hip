@@ -382,6 +382,10 @@ __device__ __forceinline__ void tile_item(
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
             int32_t p = pa, pend = lp[pa + 1].z;
+            // Without the finiteness check, the row and partial row of piece
+            // p are read when the piece starts, so its store waits on no LDS
+            // read (power-law 322K matrix, O = 8 / 32 / 128: 2% / 3% / 0.6%).
+            int32_t cur_x = lp[pa].x, cur_w = lp[pa].w;
             bool bad = false;
             auto block = [&](auto full_c, int32_t i0) {
                 constexpr bool FULL = decltype(full_c)::value;
@@ -415,12 +419,16 @@ __device__ __forceinline__ void tile_item(
                                 store_piece(lp[p], acc, k, kok);
                             }
                         } else {
-                            store_piece(lp[p], acc, k, kok);
+                            store_piece(make_int4(cur_x, 1, 0, cur_w), acc, k, kok);
                         }
 #pragma unroll
                         for (int r = 0; r < R; ++r) acc[r] = zero_vec(V());
                         ++p;
                         pend = lp[p + 1].z;
+                        if constexpr (!CHECK) {
+                            cur_x = lp[p].x;
+                            cur_w = lp[p].w;
+                        }
                     }
                 }
             };
