@@ -899,6 +899,39 @@ def test_tile_kernel_property(gpu, orc, st, M, N, bh, keep, tile_rows, fixed, O,
     assert np.linalg.norm(got - ref64) <= bound + np.linalg.norm(slack), f"{what}: rel L2"
 
 
+@settings(max_examples=60, deadline=None,
+          suppress_health_check=[HealthCheck.function_scoped_fixture, HealthCheck.too_slow])
+@given(lengths=hst.lists(hst.one_of(hst.integers(0, 4), hst.integers(5, 70),
+                                    hst.integers(60, 700)), min_size=1, max_size=90),
+       N=hst.integers(1, 900), O=hst.sampled_from([1, 2, 3, 5, 8, 32]),
+       accumulate=hst.booleans(), seed=hst.integers(0, 2 ** 31 - 1))
+def test_equal_runs_property(gpu, orc, st, lengths, N, O, accumulate, seed):
+    """Random mixes of empty, short, one-piece and split rows on single-row
+    tiles at the widths that run four work items per wave with equal stream
+    runs (O <= 8, and O = 32 with 16-byte lanes): every element of C within
+    the north-star bounds of the oracle's double sum, in both C modes
+    (accumulate: C0 + A*B, whose final FP32 rounding is allowed for)."""
+    vs = gpu
+    rng = np.random.default_rng(seed)
+    lengths = [min(k, N) for k in lengths]
+    csr = _row_lengths_csr(vs, rng, lengths, N)
+    fmt = vs.build_vcsr(csr, 4, 64, vs.LAYOUT_S)
+    fmt.set_tile_rows(1)
+    fmt.upload(st)
+    B = vs.gen_dense(int(seed % 997), 0, N, O)
+    C0 = rng.uniform(-1, 1, size=(csr.M, O)).astype(np.float32)
+    got = _ex(vs, fmt, B, C0, st, vs.KERNEL_TILE, accumulate).astype(np.float64)
+    ref64 = orc.spmm_f64(csr.M, csr.row_ptr, csr.col, csr.val, B)
+    slack = np.zeros_like(ref64)
+    if accumulate:
+        got -= C0.astype(np.float64)
+        slack = 2.0 ** -23 * np.abs(C0.astype(np.float64) + ref64)
+    what = f"M{csr.M} N{N} nnz{csr.nnz} O{O} acc{accumulate}"
+    diff = np.abs(got - ref64)
+    tol = 1e-4 * row_abs_sums(csr.row_ptr, csr.val)[:, None] * float(np.abs(B).max()) + slack
+    assert (diff <= tol).all(), f"{what}: max-abs error {float((diff - tol).max()):.3e} over tolerance"
+
+
 def test_launch_info_names_what_runs(gpu, orc, st):
     """vcsr_launch_info_get reports the default kernel's launch shape: the
     row-tile view, column slices of 256 columns (128 once B exceeds 512 MB),
