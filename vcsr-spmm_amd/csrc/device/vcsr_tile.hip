@@ -25,6 +25,10 @@
 //  - Several pieces: each stream takes a contiguous run of whole pieces
 //    (balanced by entry count), accumulates the piece's R rows and stores
 //    them when its last entry has been applied.  No cross-lane reduction.
+//    Single-row tiles with several work items per wave instead give every
+//    stream an equal run of entries; a piece cut between runs is finished
+//    by the stream that began it, from the later streams' partial sums in
+//    LDS.
 //  - One piece (a long tile): the streams interleave over its entries, whose
 //    list is padded to whole blocks, and their sums are added with
 //    cross-lane shuffles before the store.

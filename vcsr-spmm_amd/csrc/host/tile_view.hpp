@@ -38,9 +38,11 @@ constexpr int32_t kTileMmaRows = 16;
 constexpr int32_t kTileMmaGroup = 16;
 // Entries of one piece of a tile longer than half a work item (it gets work
 // items of its own): at least 64, so a long row is cut into fewer pieces
-// (and partial rows for the reduce kernel); larger pieces unbalance the
-// streams when several work items share a wave (narrow B).  The kernel's
-// LDS list holds this many entries per merged work item.
+// (and partial rows for the reduce kernel); larger pieces for single-row
+// tiles measured slower where several work items share a wave (power-law
+// 322K matrix, O = 8: 128 / 256 entries 35.1 / 48.9 against 29.2 us: the
+// wave's LDS list grows with them and fewer waves fit).  The kernel's LDS
+// list holds this many entries per merged work item.
 constexpr int32_t tile_piece_entries(int32_t R) {
     return R == kTileMmaRows ? 1024 : (32 * R > 64 ? 32 * R : 64);
 }
