@@ -578,8 +578,14 @@ def main():
         out["roofline"]["copy_gbs"] = round(copy, 1)
         out["roofline"]["frac_of_copy"] = round(achieved / copy, 4)
         if fmt is not None and args.algo in ("vcsr", "tile", "fast"):
-            # The path that binds the tile kernel: B-row slices from the caches.
-            sp = slice_path_report(w, fmt.launch_info(O, vs.KERNEL_TILE), kernel_ms)
+            # The path that binds the tile kernel: B-row slices from the
+            # caches.  A context figure only: a probe that cannot run is
+            # reported as such, not allowed to drop the line.
+            try:
+                sp = slice_path_report(w, fmt.launch_info(O, vs.KERNEL_TILE), kernel_ms)
+            except (OSError, RuntimeError) as e:
+                sp = {"error": str(e)}
+                log(f"bench: slice probe not run: {e}")
             if sp is not None:
                 out["roofline"]["b_slice_path"] = sp
     checks = [check]
