@@ -11,7 +11,9 @@
 //    kernel is compiled for (entries per item, pieces per item, rows per
 //    piece);
 //  * keep each tile's entries sorted by column (the B rows are walked in
-//    the order of the row's nonzeros).
+//    the order of the row's nonzeros);
+//  * for single-row views, put long rows' pieces in the run of work items
+//    (one per XCD) whose eighth of B holds their columns.
 // With fixed 16-row windows (the FastSpMM layout) the view must also be the
 // oracle's restatement of FastSpMM's condensed sparse tiles
 // (oracle/vcsr_oracle.cpp orc_build_cst, src/fastspmm.cu:129-251), linked in
@@ -300,6 +302,54 @@ static Csr block_matrix(uint64_t seed, int nbr, int bh, int N, int blocks, int b
     return coo_to_csr(c);
 }
 
+// Single-row views move the pieces of rows cut into 8 or more pieces into
+// the eighth of the work-item list whose eighth of B holds their middle
+// column (one run per XCD).  A banded matrix with a few long random rows:
+// the view stays valid, and nearly every moved piece sits in its run.
+static int check_long_piece_runs() {
+    Coo c;
+    c.M = 8192;
+    c.N = 8192;
+    uint64_t x = 12345;
+    auto next = [&]() {
+        x ^= x >> 12;
+        x ^= x << 25;
+        x ^= x >> 27;
+        return x * 0x2545F4914F6CDD1DULL;
+    };
+    for (int r = 0; r < c.M; ++r) {
+        const bool long_row = r % 200 == 7;
+        const int k = long_row ? 2000 : 6;
+        for (int i = 0; i < k; ++i) {
+            const int col = long_row ? (int)(next() % (uint64_t)c.N)
+                                     : std::min(c.N - 1, std::max(0, r - 60 + (int)(next() % 121)));
+            c.rows.push_back(r);
+            c.cols.push_back(col);
+            c.vals.push_back((float)((int)(next() % 201) - 100) / 64.f);
+        }
+    }
+    const Csr csr = coo_to_csr(c);
+    int bad = check(csr, 4, 64, kLayoutS, 1, 1);
+    const Vcsr v = build_vcsr(csr, 4, 64, kLayoutS, 2);
+    const TileView tv = make_tile_view(v, 1, 2, false);
+    std::vector<int> npc((size_t)csr.M, 0);
+    for (size_t i = 0; i < tv.split.size() / 4; ++i) npc[(size_t)tv.split[4 * i]] = tv.split[4 * i + 3];
+    const int nc = (int)tv.chunks.size() / 4;
+    int moved = 0, in_run = 0;
+    for (int ch = 0; ch < nc; ++ch) {
+        const int e0 = tv.chunks[4 * ch], e1 = tv.chunks[4 * ch + 1], p0 = tv.chunks[4 * ch + 2];
+        if (tv.chunks[4 * ch + 3] - p0 != 1 || tv.pieces[4 * p0 + 3] < 0) continue;
+        if (npc[(size_t)tv.pieces[4 * p0]] < 8) continue;
+        ++moved;
+        const int run = (int)((int64_t)ch * 8 / nc);
+        const int want = (int)std::min<int64_t>(7, (int64_t)tv.brow[(size_t)(e0 + (e1 - e0) / 2)] * 8 / csr.N);
+        in_run += run == want;
+    }
+    if (moved == 0 || in_run * 10 < moved * 9) bad |= fail("long pieces not in their column's run", csr.M, 1);
+    std::printf("long pieces: %d of %d in their column's run\n", in_run, moved);
+    return bad;
+}
+
 int main() {
     int bad = 0;
     const Csr cfg1 = coo_to_csr(gen_coo(1, 0));
@@ -363,6 +413,7 @@ int main() {
             }
         bad |= check_cst(coo_to_csr(g), 4, 64, kLayoutS);
     }
+    bad |= check_long_piece_runs();
     // Tiles wider than one work item (split into pieces with partial sums).
     for (int R : {1, 3, 8}) bad |= check(block_matrix(20 + R, 6, 8, 4096, 300, 4, 90, false), 4, 64, kLayoutS, R, R);
     bad |= check(block_matrix(36, 4, 16, 8192, 700, 4, 90, false), 4, 64, kLayoutS, 16, 16);

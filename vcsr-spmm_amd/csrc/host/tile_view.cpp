@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <numeric>
 #include <string>
+#include <unordered_map>
 
 #include "parallel.hpp"
 
@@ -147,6 +148,96 @@ std::vector<Tile> make_tiles(const RowLists& rl, int32_t M, int32_t cap, bool fi
     std::vector<Tile> tiles;
     for (auto& p : per) tiles.insert(tiles.end(), p.begin(), p.end());
     return tiles;
+}
+
+
+// Single-row views: the kernel hands work items to the XCDs in eight
+// contiguous runs of the item list (one per XCD, device/common.hpp
+// xcd_remap), and rows come in order, so each XCD works on an eighth of the
+// rows and, for a matrix whose columns cluster near the diagonal, on the
+// same eighth of B.  The pieces of very long rows (each an item of its own)
+// read B rows all over the matrix, but each covers a narrow column range:
+// it is moved into the run whose eighth of B holds its middle column,
+// sorted by that column among the run's other items, so that the XCD's L2
+// holds its B rows.  Run sizes stay those of the original order.
+// Rows cut into 8 or more pieces (more than 448 entries) are moved;
+// power-law 322K matrix: O = 8 / 32 / 128 25.6 / 35.9 / 107.8 ->
+// 24.9 / 33.9 / 94.8 us per SpMM.  Moving the pieces of every split row
+// (more than 64 entries) gave 25.3 / 34.7 / 98.5, from 4 or 16 pieces up
+// 25.1 / 34.3 / 95.3 and 24.9 / 34.1 / 95.4, from 32 pieces up 25.0 / 34.2
+// / 98.2.
+void order_long_pieces_by_column(TileView& tv, int32_t N) {
+    constexpr int kSeg = 8;
+    constexpr int32_t kMinPieces = 8;
+    const int32_t nc = (int32_t)(tv.chunks.size() / 4);
+    if (tv.R != 1 || nc < 4 * kSeg || N <= 0 || tv.split.empty()) return;
+    std::unordered_map<int32_t, int32_t> npc;
+    for (size_t i = 0; i < tv.split.size() / 4; ++i) npc[tv.split[4 * i]] = tv.split[4 * i + 3];
+    std::vector<int32_t> fixed;
+    std::vector<std::vector<std::pair<int32_t, int32_t>>> mov(kSeg);  // (center, chunk)
+    for (int32_t c = 0; c < nc; ++c) {
+        const int32_t e0 = tv.chunks[4 * (size_t)c], e1 = tv.chunks[4 * (size_t)c + 1];
+        const int32_t p0 = tv.chunks[4 * (size_t)c + 2], p1 = tv.chunks[4 * (size_t)c + 3];
+        bool movable = false;
+        if (p1 - p0 == 1 && tv.pieces[4 * (size_t)p0 + 3] >= 0) {
+            auto it = npc.find(tv.pieces[4 * (size_t)p0]);
+            movable = it != npc.end() && it->second >= kMinPieces;
+        }
+        if (!movable) {
+            fixed.push_back(c);
+            continue;
+        }
+        const int32_t center = tv.brow[(size_t)(e0 + (e1 - e0) / 2)];
+        const int x = (int)std::min<int64_t>(kSeg - 1, (int64_t)center * kSeg / N);
+        mov[(size_t)x].emplace_back(center, c);
+    }
+    std::vector<int32_t> order;
+    order.reserve((size_t)nc);
+    size_t f = 0;
+    for (int x = 0; x < kSeg; ++x) {
+        auto& m = mov[(size_t)x];
+        std::stable_sort(m.begin(), m.end());
+        const int64_t want = (int64_t)nc * (x + 1) / kSeg - (int64_t)nc * x / kSeg;
+        int64_t nf = x == kSeg - 1 ? (int64_t)(fixed.size() - f)
+                                   : std::max<int64_t>(0, want - (int64_t)m.size());
+        nf = std::min<int64_t>(nf, (int64_t)(fixed.size() - f));
+        // Interleave the moved pieces evenly among the run's other items.
+        const int64_t K = (int64_t)m.size();
+        int64_t j = 0;
+        for (int64_t i = 0; i < nf; ++i) {
+            while (j < K && (2 * j + 1) * nf < (2 * i + 1) * K) order.push_back(m[(size_t)j++].second);
+            order.push_back(fixed[f++]);
+        }
+        while (j < K) order.push_back(m[(size_t)j++].second);
+    }
+    while (f < fixed.size()) order.push_back(fixed[f++]);
+    TileView out;
+    out.R = tv.R;
+    out.n_tiles = tv.n_tiles;
+    out.split = tv.split;
+    out.n_partial_rows = tv.n_partial_rows;
+    const size_t E = tv.brow.size();
+    out.brow.reserve(E);
+    out.slot.reserve(E);
+    out.val.reserve(E);
+    out.mask.reserve(E);
+    out.pieces.reserve(tv.pieces.size());
+    out.chunks.reserve(tv.chunks.size());
+    for (int32_t c : order) {
+        const int32_t e0 = tv.chunks[4 * (size_t)c], e1 = tv.chunks[4 * (size_t)c + 1];
+        const int32_t p0 = tv.chunks[4 * (size_t)c + 2], p1 = tv.chunks[4 * (size_t)c + 3];
+        const int32_t ne0 = (int32_t)out.brow.size(), np0 = (int32_t)(out.pieces.size() / 4);
+        out.brow.insert(out.brow.end(), tv.brow.begin() + e0, tv.brow.begin() + e1);
+        out.slot.insert(out.slot.end(), tv.slot.begin() + e0, tv.slot.begin() + e1);
+        out.val.insert(out.val.end(), tv.val.begin() + e0, tv.val.begin() + e1);
+        out.mask.insert(out.mask.end(), tv.mask.begin() + e0, tv.mask.begin() + e1);
+        for (int32_t q = p0; q < p1; ++q)
+            out.pieces.insert(out.pieces.end(), {tv.pieces[4 * (size_t)q], tv.pieces[4 * (size_t)q + 1],
+                                                 tv.pieces[4 * (size_t)q + 2] - e0 + ne0,
+                                                 tv.pieces[4 * (size_t)q + 3]});
+        out.chunks.insert(out.chunks.end(), {ne0, ne0 + (e1 - e0), np0, np0 + (p1 - p0)});
+    }
+    tv = std::move(out);
 }
 
 }  // namespace
@@ -312,6 +403,7 @@ TileView make_tile_view(const Vcsr& v, int32_t R, int nthreads, bool fixed) {
         tv.split.swap(sorted);
     }
     tv.n_partial_rows = (int32_t)n_partial;
+    if (R == 1 && !fixed) order_long_pieces_by_column(tv, v.N);
     return tv;
 }
 
