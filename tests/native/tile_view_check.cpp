@@ -350,6 +350,21 @@ static int check_long_piece_runs() {
     return bad;
 }
 
+// The view never depends on the host thread count (rows are tiled in fixed
+// blocks; the reordering of long rows' pieces is sequential): every array
+// equal with 1 and 7 threads.
+static int check_thread_independence(const Csr& csr, int R_req, bool fixed) {
+    const Vcsr v = build_vcsr(csr, 4, 64, kLayoutS, 2);
+    const TileView a = make_tile_view(v, R_req, 1, fixed), b = make_tile_view(v, R_req, 7, fixed);
+    const bool same = a.R == b.R && a.n_tiles == b.n_tiles && a.chunks == b.chunks &&
+                      a.pieces == b.pieces && a.brow == b.brow && a.slot == b.slot &&
+                      a.mask == b.mask && a.split == b.split &&
+                      a.n_partial_rows == b.n_partial_rows && a.val.size() == b.val.size() &&
+                      std::memcmp(a.val.data(), b.val.data(), a.val.size() * sizeof(float)) == 0;
+    if (!same) return fail("view depends on the thread count", csr.M, a.R);
+    return 0;
+}
+
 int main() {
     int bad = 0;
     const Csr cfg1 = coo_to_csr(gen_coo(1, 0));
@@ -414,6 +429,12 @@ int main() {
         bad |= check_cst(coo_to_csr(g), 4, 64, kLayoutS);
     }
     bad |= check_long_piece_runs();
+    {
+        const Csr cfg3 = coo_to_csr(gen_coo(3, 0));
+        bad |= check_thread_independence(cfg3, 0, false);
+        bad |= check_thread_independence(block_matrix(41, 300, 3, 2000, 9, 3, 90, true), 0, false);
+        bad |= check_thread_independence(block_matrix(42, 40, 16, 900, 9, 16, 100, false), 16, true);
+    }
     // Tiles wider than one work item (split into pieces with partial sums).
     for (int R : {1, 3, 8}) bad |= check(block_matrix(20 + R, 6, 8, 4096, 300, 4, 90, false), 4, 64, kLayoutS, R, R);
     bad |= check(block_matrix(36, 4, 16, 8192, 700, 4, 90, false), 4, 64, kLayoutS, 16, 16);
