@@ -562,13 +562,31 @@ __device__ __forceinline__ void tile_item(
 #pragma unroll
                 for (int r = 0; r < R; ++r) acc[r] = add_vec(acc[r], shfl_xor_vec(acc[r], sh));
             }
-            // Stream 0 stores the sum, or recomputes it exactly when any of
-            // its lanes' values is not finite.
-            const bool bad = CHECK && sub == 0 && !piece_finite(acc, kok);
+            // The butterfly leaves every stream the same sums (each step adds
+            // the same two values in either order), so stream s stores rows
+            // s, s + S, ...: one store instruction per S rows instead of one
+            // per row (banded 62K matrix, O = 8: 9.9 -> 9.45 us).  A sum that
+            // is not finite is recomputed exactly by stream 0.
+            const bool bad = CHECK && !piece_finite(acc, kok);
             if (__any(bad)) {
                 if (sub == 0) redo_piece(pc1, pc1.z, ne, k, koff, kok);
-            } else if (sub == 0) {
-                store_piece(pc1, acc, k, kok);
+            } else if (kok) {
+#pragma unroll
+                for (int i = 0; i < (R + S - 1) / S; ++i) {
+                    const int r = i * S + sub;
+                    if (r < R && r < pc1.y) {
+                        V x = acc[0];
+#pragma unroll
+                        for (int q = 1; q < R; ++q)
+                            if (q == r) x = acc[q];
+                        if (pc1.w < 0) {
+                            V* dst = reinterpret_cast<V*>(C + (int64_t)(pc1.x + r) * ld + k);
+                            store_nt(dst, accumulate ? add_vec(*dst, x) : x);
+                        } else {
+                            *reinterpret_cast<V*>(partials + (int64_t)(pc1.w + r) * O + k) = x;
+                        }
+                    }
+                }
             }
         }
     }
